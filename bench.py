@@ -1,0 +1,288 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the tfp8 FP8Linear path on one MI355X.
+
+Metric: "M=1 FP8-weight GEMV HBM GB/s (% peak); M=256 fused GEMM TFLOP/s".
+`value` = GB/s of the M=1 decode GEMV on config 2 (K=4096, N=14336, bf16 activations, E4M3FN
+weights ~N(0,0.02) with 0.1% x20 outliers, K-group-128 f32 scales, bf16 out): algorithmic
+bytes (codes + scales + x + y, each crossing HBM once) / average kernel duration, measured with
+HIP events on the stream the kernel runs on. The same line carries the config-3 M=256 MFMA GEMM
+(K=N=8192, fp16 x, per-channel UE8M0, f32 bias) TFLOP/s, the decode sweep M=2/4/8, and the
+reference's CPU forward (dequantize + F.linear in fp32, restated in oracle/cpu_path.py) timed on
+the host cores of the same box.
+
+Weights rotate over >= 512 MiB of distinct copies so the 256 MB Infinity Cache cannot serve them.
+A step = one kernel launch over one batch (one copy of the layer). Synthetic data, seeded.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|gemm]
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "fp8-compatibility-layer_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_F16_TFLOPS = 2500.0     # MI355X dense fp16/bf16 MFMA
+ROTATE_BYTES = 512 << 20
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_gemv_c2_m1.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def c2_bytes(M):
+    N, K = 14336, 4096
+    return N * K + N * (K // 128) * 4 + M * K * 2 + M * N * 2
+
+
+def c3_bytes(M):
+    N = K = 8192
+    return N * K + N * 1 + N * 4 + M * K * 2 + M * N * 2
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+class Layer:
+    """One FP8 layer's device buffers plus prebuilt ctypes arguments for tfp8_linear."""
+
+    def __init__(self, lib, x, q, s, sk, G, fmt_id, bias, y, ws_buf, ws_bytes):
+        from tfp8 import _ext
+        self.fn = lib.tfp8_linear
+        M, K = x.shape
+        N = q.shape[0]
+        self.keep = (x, q, s, bias, y, ws_buf)
+        self.args = (x.data_ptr(), _ext.DTYPE_ID[x.dtype], M, K, q.data_ptr(), N, s.data_ptr(), sk, G, fmt_id,
+                     bias.data_ptr() if bias is not None else None, y.data_ptr(), _ext.DTYPE_ID[y.dtype],
+                     ws_buf.data_ptr() if ws_buf is not None else None, ws_bytes)
+
+    def __call__(self, stream):
+        rc = self.fn(*self.args, stream)
+        if rc:
+            raise RuntimeError(f"tfp8_linear rc={rc}")
+
+
+def make_layers(cfg, M, device):
+    """Rotating copies of one config's layer (>= 512 MiB of weights in total)."""
+    import torch
+
+    from tfp8 import _ext
+    from tfp8.quantize import quantize_weight
+    lib = _ext.require()
+    g = torch.Generator(device=device)
+    if cfg == "c2":
+        N, K, G, fmt, sf, pow2, xdt, ydt = 14336, 4096, 128, "e4m3fn", "f32", False, torch.bfloat16, torch.bfloat16
+        g.manual_seed(202)
+        w = torch.randn(N, K, generator=g, device=device) * 0.02
+        w = torch.where(torch.rand(N, K, generator=g, device=device) < 1e-3, w * 20, w)
+        bias = None
+    else:
+        N, K, G, fmt, sf, pow2, xdt, ydt = 8192, 8192, None, "e4m3fn", "ue8m0", True, torch.float16, torch.float16
+        g.manual_seed(303)
+        w = torch.randn(N, K, generator=g, device=device) * 0.01
+        bias = torch.randn(N, generator=g, device=device) * 0.1
+    q, s, GG = quantize_weight(w, fmt, G, pow2, sf)
+    del w
+    x = torch.randn(M, K, generator=g, device=device).to(xdt)
+    per = q.numel() + s.numel() * s.element_size()
+    copies = max(2, -(-ROTATE_BYTES // per) + 1)
+    wsb = lib.tfp8_linear_workspace_size(_ext.DTYPE_ID[xdt], M, N, K)
+    layers = []
+    for i in range(copies):
+        qi, si = (q, s) if i == 0 else (q.clone(), s.clone())
+        y = torch.empty(M, N, dtype=ydt, device=device)
+        wsbuf = torch.empty(wsb, dtype=torch.uint8, device=device) if wsb else None
+        layers.append(Layer(lib, x, qi, si, _ext.scale_kind(si), GG, _ext.FMT_ID[fmt], bias, y, wsbuf, wsb))
+    meta = dict(N=N, K=K, G=GG, fmt=fmt, scale=sf, pow2=pow2, x=str(xdt).replace("torch.", ""),
+                y=str(ydt).replace("torch.", ""), copies=copies, rotate_mib=round(copies * per / 2**20, 1))
+    return layers, (q, s, x, bias, GG, fmt), meta
+
+
+def time_layers(layers, steps, warmup):
+    """Per-launch kernel time from an event pair around every launch, plus the bracketed
+    wall time of all steps (both on torch's current stream, where the kernels run)."""
+    import torch
+    dev = torch.cuda.current_device()
+    stream = torch._C._cuda_getCurrentRawStream(dev)
+    R = len(layers)
+    for i in range(warmup):
+        layers[i % R](stream)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        a, b = ev[i]
+        a.record()
+        layers[i % R](stream)
+        b.record()
+    t1.record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) * 1e-3 for a, b in ev]          # seconds
+    total = t0.elapsed_time(t1) * 1e-3
+    return statistics.mean(per), statistics.median(per), total / steps
+
+
+def time_back_to_back(layers, steps):
+    """Total time of `steps` launches with no events between them (gives the launch-gap-inclusive rate)."""
+    import torch
+    dev = torch.cuda.current_device()
+    stream = torch._C._cuda_getCurrentRawStream(dev)
+    R = len(layers)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        layers[i % R](stream)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e-3 / steps
+
+
+def cpu_baseline(q, s, x, bias, G, fmt, nbytes, rounds=5):
+    """The reference CPU forward (oracle/cpu_path.py) on the host cores: one full C2 M=1 layer call
+    per round (weight re-materialised each call, as the reference does)."""
+    import torch
+
+    from oracle import cpu_path
+    th = cpu_threads()
+    torch.set_num_threads(th)
+    qc, sc, xc = q.cpu(), s.cpu(), x.cpu()
+    bc = bias.cpu() if bias is not None else None
+    table = cpu_path.lut16(fmt)
+    ts = []
+    for i in range(2 + rounds):
+        t = time.perf_counter()
+        cpu_path.cpu_forward(xc, qc, sc, G, fmt, bc, x.dtype, table)
+        ts.append(time.perf_counter() - t)
+    med = statistics.median(ts[2:])
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": th, "kind": "port",
+            "sample": f"full C2 M=1 layer forward (14336x4096 E4M3FN G128, bf16 x), median of {rounds} "
+                      f"rounds after 2 warm-ups, {med * 1e3:.1f} ms/call"}
+
+
+def read_traffic():
+    """HBM bytes per launch of the GEMV from the committed rocprofv3 --pmc summary, if present."""
+    try:
+        for line in open(PROFILE_TRAFFIC):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["gemv", "gemm"], default=None)
+    ap.add_argument("--sweep", action="store_true", help="also time the C2 decode sweep M=2,4,8")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {a.gpus} requested). "
+              f"Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    out = {}
+
+    # ---------------------------------------------------------------- C2 M=1 GEMV (headline)
+    if a.only in (None, "gemv"):
+        log("[bench] C2 M=1 GEMV: building rotating weights")
+        layers, (q, s, x, bias, G, fmt), meta = make_layers("c2", 1, dev)
+        mean, med, wall = time_layers(layers, a.steps, a.warmup)
+        b2b = time_back_to_back(layers, a.steps)
+        nb = c2_bytes(1)
+        gbs = nb / mean / 1e9
+        log(f"[bench] C2 M=1: kernel {mean * 1e6:.2f} us mean / {med * 1e6:.2f} us median -> {gbs:.1f} GB/s;"
+            f" back-to-back {b2b * 1e6:.2f} us/launch ({nb / b2b / 1e9:.1f} GB/s)")
+        out["gemv"] = dict(mean=mean, median=med, wall=wall, b2b=b2b, bytes=nb, gbs=gbs, meta=meta)
+        if a.sweep:
+            sweep = {}
+            for M in (2, 4, 8):
+                lm, _, _ = make_layers("c2", M, dev)
+                mm, _, _ = time_layers(lm, a.steps, a.warmup)
+                sweep[f"M{M}"] = round(c2_bytes(M) / mm / 1e9, 1)
+                log(f"[bench] C2 M={M}: {mm * 1e6:.2f} us -> {sweep[f'M{M}']} GB/s")
+                del lm
+            out["sweep"] = sweep
+        if not a.no_cpu:
+            log("[bench] CPU baseline (reference CPU forward)")
+            out["cpu"] = cpu_baseline(q, s, x, bias, G, fmt, nb)
+            log(f"[bench] CPU: {out['cpu']}")
+        del layers
+        torch.cuda.empty_cache()
+
+    # ---------------------------------------------------------------- C3 M=256 GEMM
+    if a.only in (None, "gemm"):
+        log("[bench] C3 M=256 GEMM: building rotating weights")
+        layers, _, meta3 = make_layers("c3", 256, dev)
+        steps = max(20, a.steps // 2)
+        mean3, med3, wall3 = time_layers(layers, steps, max(5, a.warmup // 2))
+        fl = 2.0 * 256 * 8192 * 8192
+        tf = fl / mean3 / 1e12
+        log(f"[bench] C3 M=256: kernel {mean3 * 1e6:.2f} us -> {tf:.1f} TFLOP/s ({c3_bytes(256) / mean3 / 1e9:.0f} GB/s)")
+        out["gemm"] = dict(mean=mean3, median=med3, wall=wall3, tflops=tf, meta=meta3)
+        del layers
+
+    g = out.get("gemv")
+    line = {
+        "metric": "M=1 FP8-weight GEMV HBM GB/s (% peak); M=256 fused GEMM TFLOP/s",
+        "value": round(g["gbs"], 1) if g else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(g["wall"] * 1e3, 5) if g else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C2 decode GEMV M=1: K=4096 N=14336, bf16 x, E4M3FN weights (0.1% x20 outliers), "
+                               "K-group-128 f32 scales, bf16 out",
+                   **({k: v for k, v in g["meta"].items()} if g else {})},
+    }
+    if g:
+        line["pct_peak_hbm"] = round(100 * g["gbs"] / PEAK_HBM_GBS, 1)
+        line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
+                            "kernel_us": round(g["mean"] * 1e6, 3), "algorithmic_bytes": g["bytes"],
+                            "back_to_back_us": round(g["b2b"] * 1e6, 3)}
+        if "sweep" in out:
+            line["decode_sweep_gbs"] = out["sweep"]
+    if "gemm" in out:
+        gm = out["gemm"]
+        line["gemm_m256"] = {"tflops": round(gm["tflops"], 1), "kernel_us": round(gm["mean"] * 1e6, 2),
+                             "roofline": {"bound": "mfma", "achieved": round(gm["tflops"], 1),
+                                          "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                                          "frac": round(gm["tflops"] / PEAK_F16_TFLOPS, 4)},
+                             "config": {"workload": "C3 fused GEMM M=256: K=N=8192, fp16 x, E4M3FN, per-channel "
+                                                    "UE8M0, f32 bias, fp16 out", **gm["meta"]}}
+    line["cpu_baseline"] = out.get("cpu")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

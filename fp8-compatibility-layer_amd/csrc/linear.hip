@@ -1,0 +1,107 @@
+// FP8Linear entry points: argument validation, path selection by M (GEMV for M <= 8, MFMA GEMM
+// above, as tfp8/_ext.py:230-253 routes), workspace layout.
+#include <stdlib.h>
+
+#include "tfp8_common.h"
+
+namespace tfp8 {
+
+int run_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind, int G,
+             int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
+int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
+             const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, float* partial,
+             hipStream_t s);
+size_t gemm_partial_bytes(int M, int N, int K);
+
+constexpr int GEMV_MAXM = 8;   // tfp8/_ext.py:37
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shared validation of the linear arguments; `what` names the entry point in messages.
+static int check_linear(const char* what, const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
+                        const void* ws, int ws_kind, int G, int fmt, const void* y, int y_dtype, bool gemm) {
+    if (M < 0 || N < 0 || K <= 0 || G <= 0)
+        return fail(TFP8_ERR_ARG, "%s: bad sizes M=%d N=%d K=%d G=%d", what, M, N, K, G);
+    if (!valid_dtype(x_dtype) || !valid_dtype(y_dtype) || !valid_fmt(fmt) || !valid_sk(ws_kind))
+        return fail(TFP8_ERR_ARG, "%s: bad enum (x_dtype=%d y_dtype=%d fmt=%d ws_kind=%d)", what, x_dtype, y_dtype,
+                    fmt, ws_kind);
+    if (K % 16 || G % 16 || K % G)
+        return fail(TFP8_ERR_SHAPE, "%s: need K %% 16 == 0, G %% 16 == 0, K %% G == 0 (K=%d G=%d)", what, K, G);
+    if (gemm && G != K && G % 32)
+        return fail(TFP8_ERR_SHAPE, "%s: the GEMM needs G == K or G %% 32 == 0 (G=%d)", what, G);
+    if (M == 0 || N == 0) return 0;
+    if (!x || !w || !ws || !y) return fail(TFP8_ERR_ARG, "%s: null pointer", what);
+    if (!aligned(x, 16) || !aligned(w, 16))
+        return fail(TFP8_ERR_ALIGN, "%s: x and w must be 16-byte aligned", what);
+    if (ws_kind == TFP8_SCALE_F32 && !aligned(ws, 4)) return fail(TFP8_ERR_ALIGN, "%s: f32 scales misaligned", what);
+    if (!aligned(y, y_dtype == TFP8_F32 ? 4 : 2)) return fail(TFP8_ERR_ALIGN, "%s: y misaligned", what);
+    return 0;
+}
+
+}  // namespace tfp8
+
+using namespace tfp8;
+
+extern "C" size_t tfp8_linear_workspace_size(int x_dtype, int M, int N, int K) {
+    if (M <= GEMV_MAXM || N <= 0 || K <= 0) return 0;
+    size_t b = 0;
+    if (x_dtype == TFP8_F32) b += align256((size_t)M * K * 2) + align256((size_t)M * 4);
+    b += gemm_partial_bytes(M, N, K);
+    return b;
+}
+
+extern "C" int tfp8_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws,
+                         int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, void* stream) {
+    clear_error();
+    if (int rc = check_linear("tfp8_gemv", x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, y, y_dtype, false)) return rc;
+    if (M > GEMV_MAXM) return fail(TFP8_ERR_ARG, "tfp8_gemv: M=%d exceeds %d", M, GEMV_MAXM);
+    if (M == 0 || N == 0) return 0;
+    return run_gemv(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, (hipStream_t)stream);
+}
+
+extern "C" int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w,
+                                  int N, const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
+                                  int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (x16_dtype != TFP8_F16 && x16_dtype != TFP8_BF16)
+        return fail(TFP8_ERR_ARG, "tfp8_gemm_prepared: activations must be f16 or bf16");
+    if (int rc = check_linear("tfp8_gemm_prepared", x16, x16_dtype, M, K, w, N, ws, ws_kind, G, fmt, y, y_dtype,
+                              true))
+        return rc;
+    if (M == 0 || N == 0) return 0;
+    const size_t need = gemm_partial_bytes(M, N, K);
+    if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
+        return fail(TFP8_ERR_WORKSPACE, "tfp8_gemm_prepared: need %zu bytes of 256-aligned workspace, got %zu",
+                    need, workspace ? workspace_bytes : (size_t)0);
+    return run_gemm(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, (float*)workspace,
+                    (hipStream_t)stream);
+}
+
+extern "C" int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws,
+                           int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    clear_error();
+    const bool gemm = M > GEMV_MAXM;
+    if (int rc = check_linear("tfp8_linear", x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, y, y_dtype, gemm))
+        return rc;
+    if (M == 0 || N == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    if (!gemm) return run_gemv(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
+
+    const size_t need = tfp8_linear_workspace_size(x_dtype, M, N, K);
+    if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
+        return fail(TFP8_ERR_WORKSPACE, "tfp8_linear: need %zu bytes of 256-aligned workspace, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+    uint8_t* wsp = (uint8_t*)workspace;
+    if (x_dtype == TFP8_F32) {
+        // fp32 activations: fp16 with an exact power-of-two row scale (tfp8/quantize.py:47-62).
+        void* x16 = wsp;
+        float* xs = (float*)(wsp + align256((size_t)M * K * 2));
+        float* part = (float*)(wsp + align256((size_t)M * K * 2) + align256((size_t)M * 4));
+        if (int rc = tfp8_prepare_activations(x, x_dtype, M, K, x16, xs, stream)) return rc;
+        return run_gemm(x16, TFP8_F16, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, part, s);
+    }
+    return run_gemm(x, x_dtype, nullptr, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, (float*)wsp, s);
+}

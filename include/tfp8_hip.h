@@ -1,0 +1,139 @@
+/*
+ * tfp8_hip.h -- C ABI of libtfp8_hip.so, the MI355X (gfx950) kernels behind the tfp8
+ * FP8Linear fused-dequant path.
+ *
+ * Every entry point is a plain host function: device pointers, sizes, enum codes and a
+ * hipStream_t passed as void*.  Nothing here allocates or frees device memory, nothing
+ * synchronises the host, and every launch is ordered on the given stream.  A return value of 0
+ * means the work was enqueued; a negative value is an argument error detected on the host
+ * before anything was launched; a positive value is a hipError_t from the launch.  The message
+ * for the last failure on the calling thread is returned by tfp8_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   tfp8/_ext.py:45-76      available()/_get(): NVRTC compile + module load per device
+ *   tfp8/_ext.py:132-157    _launch(): ctypes cuLaunchKernel with cached argument slots
+ *   tfp8/_ext.py:230-253    w8a16(): M<=8 GEMV / M>8 GEMM dispatch          -> tfp8_linear
+ *   tfp8/_ext.py:163-217    GemvLaunch (kernels tfp8_gemv_in_*_m*_*)         -> tfp8_gemv
+ *   tfp8/_ext.py:259-275    _gemm_launch()/gemm_prepared() (tfp8_gemm_*)     -> tfp8_gemm_prepared
+ *   tfp8/_ext.py:220-227    prepare_activations() (tfp8_prep_*)              -> tfp8_prepare_activations
+ *   tfp8/_ext.py:305-315    dequant_into() (tfp8_dequant_f16)                -> tfp8_dequant
+ *   tfp8/formats.py:43-69   decode()/lut() (torch, CPU/CUDA)                 -> tfp8_decode
+ *   tfp8/formats.py:77-96   encode() (torch, CPU/CUDA)                       -> tfp8_encode
+ *   tfp8/quantize.py:15-36  quantize_weight() (torch)                        -> tfp8_quantize_weight
+ *   fp8_cuda.py:85-88 + fp8_gemm_kernel.cu:22-30  UE8M0 scale encode/decode rule (scale_kind 1)
+ */
+#ifndef TFP8_HIP_H
+#define TFP8_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TFP8_ABI_VERSION 1
+
+/* Element types of activations, outputs and decoded values. */
+enum tfp8_dtype { TFP8_F16 = 0, TFP8_BF16 = 1, TFP8_F32 = 2 };
+/* FP8 code formats (tfp8/formats.py:30-31; FMT_ID in tfp8/_ext.py:41). */
+enum tfp8_fmt { TFP8_E4M3FN = 0, TFP8_E5M2 = 1 };
+/* Weight-scale storage: fp32 values, or UE8M0 bytes meaning 2^(b-127), 255 = NaN. */
+enum tfp8_scale_kind { TFP8_SCALE_F32 = 0, TFP8_SCALE_UE8M0 = 1 };
+
+/* Error codes returned before any launch. */
+#define TFP8_ERR_ARG (-1)      /* bad size, enum or null pointer */
+#define TFP8_ERR_ALIGN (-2)    /* pointer or stride not aligned as required */
+#define TFP8_ERR_SHAPE (-3)    /* K/G divisibility the kernels require */
+#define TFP8_ERR_WORKSPACE (-4) /* workspace missing or too small */
+
+/* Version of this ABI (TFP8_ABI_VERSION). */
+int tfp8_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* tfp8_last_error(void);
+
+/*
+ * out[i] = decode(q[i]) for i < n, written as f16/bf16/f32.  Exact for every code; NaN codes
+ * give a NaN, E5M2 0x7C/0xFC give +-inf.  Replaces formats.decode / formats.lut
+ * (tfp8/formats.py:43-69).  No alignment requirement.
+ */
+int tfp8_decode(const uint8_t* q, int64_t n, int fmt, void* out, int out_dtype, void* stream);
+
+/*
+ * q[i] = encode(x[i]): round-to-nearest-even, saturating to +-max_finite (never inf), NaN ->
+ * 0x7F (E4M3FN) / 0x7E (E5M2).  Same rule as formats.encode (tfp8/formats.py:77-96) and
+ * fp8.h:55-76 apart from the NaN code, which follows formats.py:94-95.
+ */
+int tfp8_encode(const void* x, int x_dtype, int64_t n, int fmt, uint8_t* q, void* stream);
+
+/*
+ * Symmetric weight quantisation, tfp8/quantize.py:15-36: for each row n and K-group g of w
+ * [N,K] (row-major, x_dtype elements), amax = max|w|, s = max(amax/max_finite, FLT_MIN),
+ * s = 2^ceil(log2 s) when pow2 (always for UE8M0), s = 1 when amax == 0, then
+ * q = encode(clamp(w/s, +-max_finite)).  scale is f32 [N, K/G] or, for TFP8_SCALE_UE8M0,
+ * uint8 [N, K/G] holding ceil(log2 s)+127 clamped to [0,254] (fp8_cuda.py:85-88).
+ * K % G == 0 required.
+ */
+int tfp8_quantize_weight(const void* w, int w_dtype, int N, int K, int G, int fmt, int pow2,
+                         int scale_kind, uint8_t* q, void* scale, void* stream);
+
+/*
+ * Activation row preparation for fp16 MFMA, tfp8/quantize.py:47-62 and _ext.py:220-227:
+ * per row, e = ceil(log2 amax) - 8 (0 if amax == 0, exact from the exponent bits),
+ * x16 = fp16(x / 2^e), xs = 2^e.  x is [M,K] f16/bf16/f32, x16 is [M,K] fp16, xs is [M] f32.
+ */
+int tfp8_prepare_activations(const void* x, int x_dtype, int M, int K, void* x16, float* xs,
+                             void* stream);
+
+/*
+ * Weight dequantisation into a caller buffer, out[n,k] = decode(w[n,k]) * scale(n, k/G), in
+ * f16/bf16/f32 (f32 is exact).  Replaces _ext.dequant_into / tfp8_dequant_f16
+ * (tfp8/_ext.py:305-315); used by tests and the module's numeric fallback, never by the
+ * forward hot path.
+ */
+int tfp8_dequant(const uint8_t* w, int N, int K, const void* ws, int ws_kind, int G, int fmt,
+                 void* out, int out_dtype, void* stream);
+
+/*
+ * y[m,n] = sum_k x[m,k] * decode(w[n,k]) * scale(n, k/G) + bias[n]  (fp32 accumulation),
+ * the FP8Linear forward (tfp8/linear.py:150-208 through _ext.w8a16, tfp8/_ext.py:230-253).
+ *
+ *   x     [M,K] row-major, x_dtype; 16-byte aligned
+ *   w     [N,K] uint8 FP8 codes row-major; 16-byte aligned, K % 16 == 0
+ *   ws    [N,K/G] f32 or UE8M0 bytes (ws_kind); G % 16 == 0, K % G == 0
+ *   bias  [N] f32 or NULL
+ *   y     [M,N] row-major, y_dtype
+ *
+ * M <= 8 runs the streaming GEMV; M > 8 runs the LDS-tiled MFMA GEMM, which additionally
+ * needs G == K or G % 32 == 0.  fp32 activations on the GEMM path are first converted to
+ * fp16 with a power-of-two row scale (tfp8_prepare_activations) in the workspace; the GEMM
+ * may also split K across blocks and keep fp32 partial sums there.  The needed size is
+ * tfp8_linear_workspace_size(); pass NULL/0 when it returns 0.  M == 0 is a no-op.
+ */
+size_t tfp8_linear_workspace_size(int x_dtype, int M, int N, int K);
+int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
+                const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
+                int y_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The GEMV alone (1 <= M <= 8), any x_dtype; GEMV kernels of tfp8/csrc/tfp8_kernels.cu:171-269. */
+int tfp8_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
+              const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
+              int y_dtype, void* stream);
+
+/*
+ * The MFMA GEMM alone on f16 or bf16 activations, with an optional per-row f32 scale xs [M]
+ * (NULL = 1), i.e. _ext.gemm_prepared (tfp8/_ext.py:267-275) / gemm_w8a16
+ * (tfp8/csrc/tfp8_kernels.cu:296-411).  Any M >= 1.  Workspace as for tfp8_linear with
+ * x_dtype = x16_dtype.
+ */
+int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, int K,
+                       const uint8_t* w, int N, const void* ws, int ws_kind, int G, int fmt,
+                       const float* bias, void* y, int y_dtype, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TFP8_HIP_H */

@@ -1,0 +1,290 @@
+"""GPU parity of the FP8Linear path (GEMV for M <= 8, MFMA GEMM above) against the float64
+oracle, with the reference's tolerance (tests/test_tfp8.py:86-89):
+
+    |y - ref| <= eps*|ref| + 1e-4*max|ref| + 1e-6,   eps = 2^-11 (fp16 out) or 2^-8 (bf16/fp32 out)
+
+Cases: the reference's kernel gates (switch points, tails, ragged K, group scales x formats x
+dtypes, pipeline edges, folded group scales, empty / non-contiguous / N-d input, prepared GEMV
+launch state, NaN fallback) and every BASELINE config at its full size, plus the reference's
+CPU dequantize-then-matmul path as a second reference.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import cpu_path
+from oracle import fp8_oracle as O
+from tfp8 import _ext
+from tfp8.linear import FP8Linear
+from tfp8.quantize import quantize_weight
+
+pytestmark = pytest.mark.gpu
+DTN = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+
+
+def _x_eff(x, path):
+    """What the kernel multiplies: x itself, except fp32 x on the GEMM path, which is fp16 with a
+    power-of-two row scale (reference prep, tfp8/quantize.py:47-62)."""
+    xf = x.float().cpu().numpy()
+    if x.dtype == torch.float32 and path == "gemm":
+        x16, xs = O.activation_to_fp16(xf)
+        return x16.astype(np.float64) * xs.astype(np.float64)[:, None]
+    return xf.astype(np.float64)
+
+
+def _check(y, x, q, s, G, fmt, bias, out_dtype, path, label):
+    ref = O.linear_ref64(_x_eff(x, path), q.cpu().numpy(), s.cpu().numpy(), G, fmt,
+                         None if bias is None else bias.cpu().numpy())
+    tol = O.tolerance(ref, DTN[out_dtype])
+    d = np.abs(y.double().cpu().numpy() - ref)
+    bad = int((~(d <= tol)).sum())
+    assert bad == 0, f"{label}: {bad} mismatches, max excess {float(np.max(d - tol)):.3g}"
+    return ref
+
+
+def _layer(N, K, G, fmt, sf="f32", pow2=True, seed=0, wscale=0.02, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * wscale
+    q, s, GG = quantize_weight(w.cuda(), fmt, G, pow2, sf)
+    b = (torch.randn(N, generator=g) * 0.1).cuda() if bias else None
+    return q, s, GG, b
+
+
+def _run(M, N, K, G, out_dtype, fmt="e4m3fn", bias=True, xdt=torch.bfloat16, sf="f32", pow2=True, seed=None):
+    seed = M * 7 + N if seed is None else seed
+    print(f"[linear] M={M} N={N} K={K} G={G} fmt={fmt} x={xdt} out={out_dtype} sf={sf} bias={bias}", flush=True)
+    q, s, GG, b = _layer(N, K, G, fmt, sf, pow2, seed, bias=bias)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(seed + 1)).to(xdt).cuda()
+    y = _ext.w8a16(x, q, None, s, b, out_dtype, GG, fmt)
+    path = "gemv" if M <= _ext.GEMV_MAXM else "gemm"
+    _check(y, x, q, s, GG, fmt, b, out_dtype, path, f"M={M} N={N} K={K} G={G} {fmt} {xdt}->{out_dtype}")
+
+
+# ------------------------------------------------------------------ reference kernel gates
+def test_kernel_switch_points_and_tails():
+    for M in (1, 2, 3, 7, 8, 9, 15, 16, 31, 32, 127, 128, 255, 256, 300):
+        _run(M, 200, 512, None, torch.float16)
+
+
+def test_kernel_ragged_k_tail():
+    for K in (528, 1040, 1152, 1168, 1184):
+        for M in (1, 8, 16, 64):
+            _run(M, 200, K, None, torch.float16)
+
+
+def test_kernel_group_scales_formats_dtypes():
+    for G in (None, 32, 128):
+        for fmt in ("e4m3fn", "e5m2"):
+            for od in (torch.float16, torch.bfloat16, torch.float32):
+                for M in (1, 40):
+                    _run(M, 128, 1024, G, od, fmt, bias=(G != 32))
+
+
+def test_activation_dtypes_both_paths():
+    for xdt in (torch.float16, torch.bfloat16, torch.float32):
+        for M in (1, 3, 8, 9, 33, 100):
+            for sf in ("f32", "ue8m0"):
+                _run(M, 160, 768, 128, torch.float32, "e4m3fn", xdt=xdt, sf=sf)
+
+
+def test_gemm_pipeline_edges():
+    for K in (32, 64, 96, 160):
+        for G in (None, 32):
+            for M in (9, 64, 65, 130):
+                _run(M, 72, K, G, torch.float16, bias=(G is None))
+
+
+def test_group_scale_applied_per_block():
+    print("[group locality]", flush=True)
+    K, N = 256, 64
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(N, K, generator=g) * 0.02
+    w[:, :128] *= 1000.0
+    q, s, G = quantize_weight(w.cuda(), "e4m3fn", 128)
+    x = (torch.randn(33, K, generator=g) * 1e-3).cuda()
+    for M in (1, 33):
+        y = _ext.w8a16(x[:M], q, None, s, None, torch.float16, G, "e4m3fn")
+        ref = O.linear_ref64(x[:M].cpu().numpy(), q.cpu().numpy(), s.cpu().numpy(), G, "e4m3fn")
+        assert (np.abs(y.double().cpu().numpy() - ref) / np.abs(ref).max()).max() < 2e-3
+
+
+def test_gemm_group_scales_exact_fp32_partials():
+    """K-group scales spanning 2^-20 (pow2) and arbitrary f32 values (checkpoint mode) are applied to
+    fp32 partial sums, so the error stays at fp32-accumulation level in both cases -- tighter than
+    the reference's fold-into-fp16 bound (1e-5 / 5e-4 relative to the largest output)."""
+    g = torch.Generator().manual_seed(5)
+    N, K, G = 96, 1024, 128
+    for fmt in ("e4m3fn", "e5m2"):
+        for pow2 in (True, False):
+            print(f"[folded scales] fmt={fmt} pow2={pow2}", flush=True)
+            codes = torch.randint(0, 256, (N, K), dtype=torch.uint8, generator=g)
+            v = torch.from_numpy(O.decode(codes.numpy(), fmt))
+            codes[~torch.isfinite(v)] = 0x10
+            ws = torch.exp2(torch.randint(-20, 1, (N, K // G), generator=g).float()) * 1e-2
+            if not pow2:
+                ws = ws * (1 + torch.rand(N, K // G, generator=g))
+            f = FP8Linear.from_fp8_checkpoint(codes.cuda(), ws.cuda(), bias=torch.randn(N, generator=g).cuda(),
+                                              fmt=fmt)
+            f.out_dtype = torch.float32
+            f.nan_check = False
+            for M in (16, 100):
+                x = torch.randn(M, K, generator=g).bfloat16().cuda()
+                ref = O.linear_ref64(x.float().cpu().numpy(), codes.numpy(), ws.numpy(), G, fmt, f.bias_f32.cpu().numpy())
+                err = (np.abs(f(x).double().cpu().numpy() - ref) / np.abs(ref).max()).max()
+                assert err < 1e-5, f"{fmt} pow2={pow2} M={M}: err/max {err}"
+            assert f.stats["gemm"] >= 1
+
+
+def test_forced_gemm_at_small_m_and_gemv_directly():
+    """The MFMA GEMM at M <= 8 (gemm_prepared) and the GEMV entry point agree with the oracle."""
+    q, s, G, b = _layer(136, 512, 64, "e5m2", "ue8m0", seed=21)
+    for M in (1, 5, 8):
+        print(f"[forced paths] M={M}", flush=True)
+        x = torch.randn(M, 512, generator=torch.Generator().manual_seed(M)).half().cuda()
+        y1 = _ext.gemm_prepared(x, None, q, None, s, b, torch.float32, G, "e5m2")
+        _check(y1, x, q, s, G, "e5m2", b, torch.float32, "gemm", f"gemm M={M}")
+        xs = torch.full((M,), 0.5, device="cuda")
+        y2 = _ext.gemm_prepared(x, xs, q, None, s, b, torch.float32, G, "e5m2")
+        ref = O.linear_ref64(x.float().cpu().numpy() * 0.5, q.cpu().numpy(), s.cpu().numpy(), G, "e5m2",
+                             b.cpu().numpy())
+        assert (np.abs(y2.double().cpu().numpy() - ref) <= O.tolerance(ref, "float32")).all()
+        y3 = _ext.gemv(x, q, s, b, torch.float32, G, "e5m2")
+        _check(y3, x, q, s, G, "e5m2", b, torch.float32, "gemv", f"gemv M={M}")
+
+
+def test_gemv_prepared_launch_tracks_layer_state():
+    print("[gemv launch state]", flush=True)
+    torch.manual_seed(11)
+    lin = nn.Linear(512, 200, device="cuda")
+    f = FP8Linear.from_linear(lin, group_size=128)
+    f.nan_check = False
+
+    def general(x):
+        return _ext.w8a16(x.reshape(-1, 512), f.qweight, None, f.weight_scale, f.bias_f32, f.out_dtype,
+                          f.group_size, f.fmt)
+
+    for xd in (torch.float16, torch.bfloat16, torch.float32):
+        for M in (1, 3, 8):
+            x = torch.randn(M, 512, device="cuda", dtype=xd)
+            y = f(x)
+            assert torch.equal(y, general(x)), (xd, M)
+            _check(y, x, f.qweight, f.weight_scale, 128, "e4m3fn", f.bias_f32, f.out_dtype, "gemv", f"{xd} M={M}")
+    assert len(f._gemv) == 3
+    x = torch.randn(2, 3, 512, device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(f(x), general(x).reshape(2, 3, 200))
+    x = torch.randn(4, 512, device="cuda", dtype=torch.bfloat16)
+    f.out_dtype = torch.float16
+    assert f(x).dtype == torch.float16 and torch.equal(f(x), general(x))
+    other = FP8Linear.from_linear(nn.Linear(512, 200, device="cuda"), group_size=128)
+    f.qweight = other.qweight.clone()
+    f.weight_scale = other.weight_scale.clone()
+    assert torch.equal(f(x), general(x))
+    f.load_state_dict(other.state_dict())
+    assert torch.equal(f(x), general(x))
+    f.cpu()
+    assert f(x.cpu()).device.type == "cpu"
+    f.cuda()
+    y = f(x)
+    assert torch.equal(y, general(x)) and f.stats["gemv"] >= 12
+
+
+def test_empty_and_noncontiguous():
+    print("[empty/noncontig]", flush=True)
+    f = FP8Linear.from_linear(nn.Linear(512, 128, device="cuda"))
+    assert f(torch.empty(0, 512, device="cuda")).shape == (0, 128)
+    x = torch.randn(512, 20, device="cuda").t()
+    assert torch.allclose(f(x).float(), f(x.contiguous()).float())
+    assert f(torch.randn(2, 3, 512, device="cuda")).shape == (2, 3, 128)
+    assert f(torch.randn(3, 7, 512, device="cuda")).shape == (3, 7, 128)   # M=21 -> GEMM
+
+
+def test_nan_fallback():
+    print("[nan fallback]", flush=True)
+    f = FP8Linear.from_linear(nn.Linear(512, 128, device="cuda"))
+    f.out_dtype = torch.float16
+    f.weight_scale.fill_(1e30)
+    f(torch.randn(4, 512, device="cuda"))
+    assert f.fallback is not None and "non-finite" in f.fallback_reason
+
+
+def test_chunked_backend_counts_and_matches():
+    print("[large-M branch]", flush=True)
+    torch.manual_seed(7)
+    lin = nn.Linear(1024, 330, device="cuda")
+    f = FP8Linear.from_linear(lin, large_m_backend="chunked")
+    f.out_dtype = torch.float16
+    x = torch.randn(300, 1024, device="cuda", dtype=torch.bfloat16)
+    y = f(x)
+    assert f.stats["chunked"] == 1
+    _check(y, x, f.qweight, f.weight_scale, 1024, "e4m3fn", f.bias_f32, torch.float16, "gemm", "chunked")
+
+
+# ------------------------------------------------------------------ BASELINE configs, full size
+def test_config1_gemv_m1_and_cpu_path():
+    """C1: M=1, K=N=4096, fp16 x ~N(0,1), W ~N(0,0.02) E4M3FN per-channel pow2 f32, no bias."""
+    print("[C1] M=1 K=N=4096", flush=True)
+    g = torch.Generator().manual_seed(101)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    q, s, G = quantize_weight(w.cuda(), "e4m3fn", None, True)
+    x = torch.randn(1, 4096, generator=g).half()
+    f = FP8Linear.from_fp8_checkpoint(q, s, fmt="e4m3fn")
+    f.out_dtype = torch.float16
+    f.nan_check = False
+    y = f(x.cuda())
+    assert f.stats["gemv"] == 1
+    _check(y, x, q, s, G, "e4m3fn", None, torch.float16, "gemv", "C1")
+    # the reference's own CPU path (dequantize then F.linear in fp32) within the same bound
+    yc = cpu_path.cpu_forward(x, q.cpu(), s.cpu(), G, "e4m3fn", None, torch.float32).double().numpy()
+    d = np.abs(y.double().cpu().numpy() - yc)
+    assert (d <= O.tolerance(yc, "float16")).all()
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_config2_decode_sweep(M):
+    """C2: K=4096, N=14336, bf16 x, W ~N(0,0.02) with 0.1% outliers x20, E4M3FN G=128 f32 scales
+    (general amax/448 and the pow2 side check)."""
+    print(f"[C2] M={M}", flush=True)
+    g = torch.Generator().manual_seed(202)
+    w = torch.randn(14336, 4096, generator=g) * 0.02
+    w = torch.where(torch.rand(w.shape, generator=g) < 1e-3, w * 20, w)
+    x = torch.randn(M, 4096, generator=g).bfloat16().cuda()
+    for pow2 in (False, True):
+        q, s, G = quantize_weight(w.cuda(), "e4m3fn", 128, pow2)
+        y = _ext.w8a16(x, q, None, s, None, torch.bfloat16, G, "e4m3fn")
+        _check(y, x, q, s, G, "e4m3fn", None, torch.bfloat16, "gemv", f"C2 M={M} pow2={pow2}")
+
+
+@pytest.mark.parametrize("M", [16, 64, 256])
+def test_config3_gemm(M):
+    """C3: K=N=8192, fp16 x, E4M3FN W ~N(0,0.01) per-channel UE8M0, f32 bias ~N(0,0.1)."""
+    print(f"[C3] M={M}", flush=True)
+    g = torch.Generator().manual_seed(303)
+    w = torch.randn(8192, 8192, generator=g) * 0.01
+    q, s, G = quantize_weight(w.cuda(), "e4m3fn", None, True, "ue8m0")
+    b = (torch.randn(8192, generator=g) * 0.1).cuda()
+    x = torch.randn(M, 8192, generator=g).half().cuda()
+    y = _ext.w8a16(x, q, None, s, b, torch.float16, G, "e4m3fn")
+    _check(y, x, q, s, G, "e4m3fn", b, torch.float16, "gemm", f"C3 M={M}")
+
+
+def test_config4_e5m2_block32_ue8m0():
+    """C4: M=128, K=11008, N=4096, bf16 x rows scaled by 2^u (u in -20..20), W ~Laplace(0,0.02)
+    E5M2 with G=32 UE8M0 scales; forced +-0, subnormal codes 0x01-0x03/0x81-0x83 and max codes."""
+    print("[C4] M=128 K=11008 N=4096 e5m2 G32 ue8m0", flush=True)
+    g = torch.Generator().manual_seed(404)
+    w = torch.distributions.Laplace(0.0, 0.02).sample((4096, 11008))
+    q, s, G = quantize_weight(w.cuda(), "e5m2", 32, True, "ue8m0")
+    q = q.cpu()
+    idx = torch.randint(0, q.numel(), (4096,), generator=g)
+    special = torch.tensor([0x00, 0x80, 0x01, 0x02, 0x03, 0x81, 0x82, 0x83, 0x7B, 0xFB], dtype=torch.uint8)
+    q.view(-1)[idx] = special[torch.arange(4096) % len(special)]
+    q = q.cuda()
+    u = torch.randint(-20, 21, (128, 1), generator=g).float()
+    x = (torch.randn(128, 11008, generator=g) * torch.exp2(u)).bfloat16().cuda()
+    y = _ext.w8a16(x, q, None, s, None, torch.bfloat16, G, "e5m2")
+    _check(y, x, q, s, G, "e5m2", None, torch.bfloat16, "gemm", "C4")
+    # the encoder side of C4: saturation of +-1e9 / +-inf and E5M2 subnormals
+    t = torch.tensor([1e9, -1e9, float("inf"), -float("inf"), 2.0 ** -16, -(2.0 ** -15), 3 * 2.0 ** -16, 0.0, -0.0])
+    from tfp8.formats import encode
+    assert torch.equal(encode(t.cuda(), "e5m2").cpu(), torch.from_numpy(O.encode(t.numpy(), "e5m2")))

@@ -1,0 +1,247 @@
+"""CPU-side tests: the tfp8 package's CPU paths against the oracle, the module/planner API
+(reference tests/test_tfp8.py:29-72, 278-319), and the C-ABI library's exports and host-side
+argument validation (no kernel is launched here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import tfp8
+from oracle import fp8_oracle as O
+from tfp8 import _ext
+from tfp8.formats import E4M3FN, E5M2, decode, encode, lut
+from tfp8.linear import FP8Linear
+from tfp8.quantize import activation_to_fp16, dequantize_weight, quantize_weight
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tfp8_hip.h")
+FMTS = (E4M3FN, E5M2)
+
+
+def _same(a, b):
+    a, b = a.float(), b.float()
+    both_nan = torch.isnan(a) & torch.isnan(b)
+    eq = (a == b) & (torch.signbit(a) == torch.signbit(b))
+    return bool((both_nan | eq).all())
+
+
+# ------------------------------------------------------------------ formats (CPU paths)
+@pytest.mark.parametrize("f", FMTS, ids=lambda f: f.name)
+def test_cpu_decode_and_lut_match_oracle(f):
+    codes = torch.arange(256, dtype=torch.uint8)
+    assert _same(decode(codes, f), torch.from_numpy(O.decode(np.arange(256), f.name)))
+    assert _same(lut(f).float(), codes.view(f.torch_dtype).float())
+
+
+@pytest.mark.parametrize("f", FMTS, ids=lambda f: f.name)
+def test_cpu_encode_matches_oracle_and_torch(f):
+    torch.manual_seed(0)
+    x = torch.cat([torch.randn(20000) * f.max_finite / 8, torch.randn(2000) * 2.0 ** -10,
+                   torch.tensor([1e9, -1e9, float("inf"), -float("inf"), float("nan"), 0.0, -0.0])])
+    got = encode(x, f)
+    assert torch.equal(got, torch.from_numpy(O.encode(x.numpy(), f.name)))
+    inr = x.abs() < f.max_finite
+    assert torch.equal(got[inr], x[inr].to(f.torch_dtype).view(torch.uint8))
+    for dt in (torch.float16, torch.bfloat16, torch.float64):
+        xd = x.to(dt)
+        assert torch.equal(encode(xd, f), torch.from_numpy(O.encode(xd.double().numpy(), f.name)))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+@pytest.mark.parametrize("G", [None, 32, 128])
+@pytest.mark.parametrize("sf", ["f32", "ue8m0"])
+def test_cpu_quantize_matches_oracle(fmt, G, sf):
+    torch.manual_seed(1)
+    w = torch.randn(40, 256) * 0.02
+    w[1] = 0
+    q, s, GG = quantize_weight(w, fmt, G, True, sf)
+    oq, os_, _ = O.quantize_weight(w.numpy(), fmt, G, True, sf)
+    assert torch.equal(q, torch.from_numpy(oq)) and torch.equal(s, torch.from_numpy(os_))
+    d = dequantize_weight(q, s, fmt, GG)
+    assert torch.equal(d, torch.from_numpy(O.dequantize_weight(oq, os_, fmt, GG)))
+
+
+def test_cpu_quantize_nonpow2_matches_oracle():
+    torch.manual_seed(2)
+    w = torch.randn(24, 128) * 0.05
+    q, s, G = quantize_weight(w, "e4m3fn", 32, False)
+    oq, os_, _ = O.quantize_weight(w.numpy(), "e4m3fn", 32, False)
+    assert torch.equal(q, torch.from_numpy(oq)) and torch.equal(s, torch.from_numpy(os_))
+
+
+def test_activation_scaling_is_exact_power_of_two():
+    x = (torch.randn(5, 256) * 1e3).bfloat16()
+    x16, xs = activation_to_fp16(x)
+    assert torch.all(torch.log2(xs) == torch.round(torch.log2(xs)))
+    assert torch.equal((x16.float() * xs[:, None]), x.float())
+    ox16, oxs = O.activation_to_fp16(x.float().numpy())
+    assert torch.equal(xs, torch.from_numpy(oxs)) and torch.equal(x16, torch.from_numpy(ox16))
+
+
+# ------------------------------------------------------------------ module / planner
+def test_cpu_reference_path():
+    lin = nn.Linear(256, 64)
+    f = FP8Linear.from_linear(lin, group_size=128)
+    x = torch.randn(3, 256)
+    y = f(x)
+    ref = x @ f.dequantized_weight().t() + lin.bias
+    assert torch.allclose(y.float(), ref, atol=1e-2, rtol=1e-2)
+    assert f.stats["torch"] == 1
+
+
+def test_cpu_path_matches_oracle_ue8m0():
+    torch.manual_seed(9)
+    lin = nn.Linear(256, 96)
+    f = FP8Linear.from_linear(lin, fmt="e5m2", group_size=32, scale_format="ue8m0")
+    assert f.weight_scale.dtype == torch.uint8
+    f.out_dtype = torch.float32
+    x = torch.randn(4, 256)
+    ref = O.linear_ref64(x.numpy(), f.qweight.numpy(), f.weight_scale.numpy(), 32, "e5m2", f.bias_f32.numpy())
+    d = np.abs(f(x).double().numpy() - ref)
+    assert (d <= O.tolerance(ref, "float32")).all()
+
+
+def test_planner_policy_and_tied_weights():
+    class Block(nn.Module):
+        def __init__(s):
+            super().__init__()
+            s.q_proj, s.o_proj = nn.Linear(1024, 1024), nn.Linear(1024, 1024)
+            s.gate_proj = nn.Linear(1024, 2048)
+            s.input_layernorm = nn.LayerNorm(1024)
+            s.lora_A = nn.Linear(1024, 8)
+            s.router = nn.Linear(1024, 1024)
+
+    class LM(nn.Module):
+        def __init__(s):
+            super().__init__()
+            s.embed = nn.Embedding(100, 1024)
+            s.layers = nn.ModuleList([Block()])
+            s.lm_head = nn.Linear(1024, 100, bias=False)
+            s.lm_head.weight = s.embed.weight
+
+    m = tfp8.prepare_model(LM(), "llm", tfp8.FP8Config(profile="llm_safe"))
+    owners = {d.name: d.owner for d in m._tfp8_plan}
+    reasons = {d.name: d.reason for d in m._tfp8_plan}
+    text = tfp8.report(m, file=open(os.devnull, "w"))
+    assert owners["layers.0.q_proj"] == "tfp8" and owners["layers.0.gate_proj"] == "tfp8"
+    assert owners["layers.0.lora_A"] != "tfp8" and owners["layers.0.router"] != "tfp8"
+    assert owners["lm_head"] != "tfp8"
+    assert m.lm_head.weight is m.embed.weight
+    assert isinstance(m.layers[0].q_proj, FP8Linear)
+    again = tfp8.prepare_model(m, "llm", tfp8.FP8Config())
+    assert {d.name: d.owner for d in again._tfp8_plan}["layers.0.q_proj"] == "tfp8"
+    assert isinstance(again.layers[0].q_proj, FP8Linear)
+    assert reasons["lm_head"] == "weight shared with another module (tied)"
+    assert reasons["layers.0.lora_A"] == "'lora_A' is precision-sensitive"
+    assert "-- 3/6 Linear modules on tfp8" in text
+    wb = tfp8.weight_bytes(m)
+    assert wb["uint8"] == 1024 * 1024 * 2 + 2048 * 1024
+
+
+def test_planner_ue8m0_and_groups():
+    class M(nn.Module):
+        def __init__(s):
+            super().__init__()
+            s.up_proj = nn.Linear(1024, 2048)
+            s.small_mlp = nn.Linear(1024, 512)
+
+    m = tfp8.prepare_model(M(), "llm", tfp8.FP8Config(weight_group=128, scale_format="ue8m0", fmt="e5m2"))
+    assert isinstance(m.up_proj, FP8Linear) and m.up_proj.weight_scale.dtype == torch.uint8
+    assert m.up_proj.weight_scale.shape == (2048, 8) and m.up_proj.fmt == "e5m2"
+    assert not isinstance(m.small_mlp, FP8Linear)
+
+
+def test_config_validation():
+    with pytest.raises(ValueError):
+        tfp8.FP8Config(profile="fast")
+    with pytest.raises(NotImplementedError):
+        tfp8.FP8Config(activation="fp8")
+    with pytest.raises(NotImplementedError):
+        tfp8.FP8Config(kv_cache="fp8")
+    with pytest.raises(ValueError):
+        tfp8.FP8Config(large_m_backend="cublas")
+    with pytest.raises(ValueError):
+        tfp8.FP8Config(scale_format="e4m3")
+    assert tfp8.FP8Config(profile="image_safe").min_features == 256
+
+
+def test_checkpoint_compat_mode_keeps_codes():
+    q = torch.randint(0, 256, (64, 128), dtype=torch.uint8)
+    q[E4M3FN.is_nan(q.int())] = 0
+    s = torch.rand(64) + 0.5
+    f = FP8Linear.from_fp8_checkpoint(q.view(torch.float8_e4m3fn), s, fmt="e4m3fn")
+    assert torch.equal(f.qweight, q) and torch.equal(f.weight_scale[:, 0], s)
+    with pytest.raises(ValueError):
+        FP8Linear.from_fp8_checkpoint(q.view(torch.float8_e4m3fn), s, fmt="e5m2")
+    # per-tensor (scalar) and per-K-group UE8M0 scales
+    ft = FP8Linear.from_fp8_checkpoint(q, torch.tensor(0.25), fmt="e4m3fn")
+    assert ft.weight_scale.shape == (64, 1) and bool((ft.weight_scale == 0.25).all())
+    b = torch.randint(100, 140, (64, 4), dtype=torch.uint8)
+    fg = FP8Linear.from_fp8_checkpoint(q, b, fmt="e4m3fn")
+    assert fg.group_size == 32 and fg.weight_scale.dtype == torch.uint8 and torch.equal(fg.weight_scale, b)
+    x = torch.randn(2, 128)
+    ref = O.linear_ref64(x.numpy(), q.numpy(), b.numpy(), 32, "e4m3fn")
+    assert fg.out_dtype == torch.bfloat16                    # reference default out dtype
+    assert bool((np.abs(fg(x).double().numpy() - ref) <= O.tolerance(ref, "bfloat16")).all())
+
+
+def test_unsupported_shapes_take_torch_path():
+    f = FP8Linear(40, 16, group_size=8)     # K % 16 != 0: no kernel takes it
+    assert not f._kernels_ok
+    assert FP8Linear(256, 16, group_size=16)._kernels_ok is False   # G=16: GEMM needs G % 32
+    assert FP8Linear(528, 16)._kernels_ok                            # K % 16 == 0, per-channel
+
+
+# ------------------------------------------------------------------ C ABI
+def _header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(tfp8_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    names = _header_functions()
+    assert len(names) == 11, names
+    lib = ctypes.CDLL(_ext.lib_path())
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(_ext._SIGS) == names          # every entry point bound with argtypes
+    assert _ext.library().tfp8_abi_version() == _ext.ABI_VERSION
+
+
+def test_abi_argument_validation_without_gpu():
+    lib = _ext.library()
+    assert lib.tfp8_decode(None, -1, 0, None, 0, None) == -1
+    assert b"bad n/fmt" in lib.tfp8_last_error()
+    assert lib.tfp8_decode(None, 0, 0, None, 0, None) == 0          # n == 0 is a no-op
+    assert lib.tfp8_encode(None, 9, 4, 0, None, None) == -1
+    # K % 16
+    rc = lib.tfp8_linear(None, 1, 1, 40, None, 8, None, 0, 40, 0, None, None, 1, None, 0, None)
+    assert rc == -3 and b"K % 16" in lib.tfp8_last_error()
+    # G neither K nor a multiple of 32 on the GEMM path
+    rc = lib.tfp8_linear(None, 1, 64, 256, None, 8, None, 0, 16, 0, None, None, 1, None, 0, None)
+    assert rc == -3 and b"G == K or G % 32" in lib.tfp8_last_error()
+    # M > 8 with a missing workspace must be refused before launching (needs pointers first)
+    assert lib.tfp8_gemv(None, 1, 9, 256, None, 8, None, 0, 256, 0, None, None, 1, None) == -1
+    # null pointers with real sizes
+    rc = lib.tfp8_linear(None, 1, 4, 256, None, 8, None, 0, 256, 0, None, None, 1, None, 0, None)
+    assert rc == -1 and b"null pointer" in lib.tfp8_last_error()
+    # misaligned x
+    buf = ctypes.create_string_buffer(4096)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    rc = lib.tfp8_linear(base + 2, 1, 4, 256, base, 8, base, 0, 256, 0, None, base, 1, None, 0, None)
+    assert rc == -2
+    assert lib.tfp8_quantize_weight(None, 2, 4, 100, 32, 0, 1, 0, None, None, None) == -3
+    assert lib.tfp8_linear_workspace_size(2, 4, 128, 256) == 0          # GEMV needs none
+    assert lib.tfp8_linear_workspace_size(2, 64, 128, 256) >= 64 * 256 * 2   # fp32 prep buffer
+
+
+def test_available_false_and_require_raises_without_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert _ext.available() is False
+    with pytest.raises(RuntimeError):
+        _ext.require()
