@@ -16,7 +16,6 @@ A step = one kernel launch over one batch (one copy of the layer). Synthetic dat
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|gemm]
 """
 import argparse
-import ctypes
 import json
 import os
 import statistics
@@ -40,6 +39,11 @@ def log(*a):
 def c2_bytes(M):
     N, K = 14336, 4096
     return N * K + N * (K // 128) * 4 + M * K * 2 + M * N * 2
+
+
+def c1_bytes(M):
+    N = K = 4096
+    return N * K + N * 4 + M * K * 2 + M * N * 2
 
 
 def c3_bytes(M):
@@ -82,7 +86,12 @@ def make_layers(cfg, M, device):
     from tfp8.quantize import quantize_weight
     lib = _ext.require()
     g = torch.Generator(device=device)
-    if cfg == "c2":
+    if cfg == "c1":
+        N, K, G, fmt, sf, pow2, xdt, ydt = 4096, 4096, None, "e4m3fn", "f32", True, torch.float16, torch.float16
+        g.manual_seed(101)
+        w = torch.randn(N, K, generator=g, device=device) * 0.02
+        bias = None
+    elif cfg == "c2":
         N, K, G, fmt, sf, pow2, xdt, ydt = 14336, 4096, 128, "e4m3fn", "f32", False, torch.bfloat16, torch.bfloat16
         g.manual_seed(202)
         w = torch.randn(N, K, generator=g, device=device) * 0.02
@@ -110,46 +119,51 @@ def make_layers(cfg, M, device):
     return layers, (q, s, x, bias, GG, fmt), meta
 
 
+_SLEEP_CYCLES = None
+
+
+def _queue_ahead_cycles():
+    """Cycles for torch.cuda._sleep to cover ~40 ms, calibrated once with events."""
+    global _SLEEP_CYCLES
+    if _SLEEP_CYCLES is None:
+        import torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(1_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        per_cycle = max(a.elapsed_time(b) * 1e-3 / 1e6, 1e-11)
+        _SLEEP_CYCLES = int(0.04 / per_cycle)
+    return _SLEEP_CYCLES
+
+
 def time_layers(layers, steps, warmup):
-    """Per-launch kernel time from an event pair around every launch, plus the bracketed
-    wall time of all steps (both on torch's current stream, where the kernels run)."""
+    """Average launch duration: `steps` back-to-back launches between two events on the stream
+    the kernels run on (torch's current stream). A bounded sleep kernel is queued first so the
+    host has enqueued every launch before the first one starts -- the interval then holds only
+    the kernels and the GPU's own dispatch gaps, not Python's launch rate."""
     import torch
     dev = torch.cuda.current_device()
     stream = torch._C._cuda_getCurrentRawStream(dev)
     R = len(layers)
     for i in range(warmup):
         layers[i % R](stream)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    cycles = _queue_ahead_cycles()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    torch.cuda._sleep(cycles)
     t0.record()
+    h0 = time.perf_counter()
     for i in range(steps):
-        a, b = ev[i]
-        a.record()
         layers[i % R](stream)
-        b.record()
     t1.record()
+    host = time.perf_counter() - h0
     torch.cuda.synchronize()
-    per = [a.elapsed_time(b) * 1e-3 for a, b in ev]          # seconds
     total = t0.elapsed_time(t1) * 1e-3
-    return statistics.mean(per), statistics.median(per), total / steps
-
-
-def time_back_to_back(layers, steps):
-    """Total time of `steps` launches with no events between them (gives the launch-gap-inclusive rate)."""
-    import torch
-    dev = torch.cuda.current_device()
-    stream = torch._C._cuda_getCurrentRawStream(dev)
-    R = len(layers)
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    for i in range(steps):
-        layers[i % R](stream)
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) * 1e-3 / steps
+    if host > 0.035:
+        log(f"[bench] warning: enqueue took {host * 1e3:.1f} ms, longer than the queued sleep")
+    return total / steps
 
 
 def cpu_baseline(q, s, x, bias, G, fmt, nbytes, rounds=5):
@@ -192,7 +206,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm"], default=None)
-    ap.add_argument("--sweep", action="store_true", help="also time the C2 decode sweep M=2,4,8")
+    ap.add_argument("--sweep", action="store_true", help="also time the C2 decode sweep M=2,4,8 and C3 M=16,64")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run torch copies of a 256 MiB buffer (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {a.gpus} requested). "
@@ -206,23 +223,34 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     out = {}
+    if a.calibrate_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] calibration: 5 copies of 268435456 bytes (read + write each)")
+        return
 
     # ---------------------------------------------------------------- C2 M=1 GEMV (headline)
     if a.only in (None, "gemv"):
         log("[bench] C2 M=1 GEMV: building rotating weights")
         layers, (q, s, x, bias, G, fmt), meta = make_layers("c2", 1, dev)
-        mean, med, wall = time_layers(layers, a.steps, a.warmup)
-        b2b = time_back_to_back(layers, a.steps)
+        mean = time_layers(layers, a.steps, a.warmup)
         nb = c2_bytes(1)
         gbs = nb / mean / 1e9
-        log(f"[bench] C2 M=1: kernel {mean * 1e6:.2f} us mean / {med * 1e6:.2f} us median -> {gbs:.1f} GB/s;"
-            f" back-to-back {b2b * 1e6:.2f} us/launch ({nb / b2b / 1e9:.1f} GB/s)")
-        out["gemv"] = dict(mean=mean, median=med, wall=wall, b2b=b2b, bytes=nb, gbs=gbs, meta=meta)
+        log(f"[bench] C2 M=1: {mean * 1e6:.2f} us/launch -> {gbs:.1f} GB/s")
+        out["gemv"] = dict(mean=mean, bytes=nb, gbs=gbs, meta=meta)
+        l1, _, _ = make_layers("c1", 1, dev)
+        m1 = time_layers(l1, a.steps, a.warmup)
+        out["c1"] = dict(us=m1 * 1e6, gbs=c1_bytes(1) / m1 / 1e9)
+        log(f"[bench] C1 M=1: {m1 * 1e6:.2f} us/launch -> {out['c1']['gbs']:.1f} GB/s")
+        del l1
         if a.sweep:
             sweep = {}
             for M in (2, 4, 8):
                 lm, _, _ = make_layers("c2", M, dev)
-                mm, _, _ = time_layers(lm, a.steps, a.warmup)
+                mm = time_layers(lm, a.steps, a.warmup)
                 sweep[f"M{M}"] = round(c2_bytes(M) / mm / 1e9, 1)
                 log(f"[bench] C2 M={M}: {mm * 1e6:.2f} us -> {sweep[f'M{M}']} GB/s")
                 del lm
@@ -239,11 +267,20 @@ def main():
         log("[bench] C3 M=256 GEMM: building rotating weights")
         layers, _, meta3 = make_layers("c3", 256, dev)
         steps = max(20, a.steps // 2)
-        mean3, med3, wall3 = time_layers(layers, steps, max(5, a.warmup // 2))
+        mean3 = time_layers(layers, steps, max(5, a.warmup // 2))
         fl = 2.0 * 256 * 8192 * 8192
         tf = fl / mean3 / 1e12
         log(f"[bench] C3 M=256: kernel {mean3 * 1e6:.2f} us -> {tf:.1f} TFLOP/s ({c3_bytes(256) / mean3 / 1e9:.0f} GB/s)")
-        out["gemm"] = dict(mean=mean3, median=med3, wall=wall3, tflops=tf, meta=meta3)
+        out["gemm"] = dict(mean=mean3, tflops=tf, meta=meta3)
+        gsweep = {}
+        for M in ((16, 64) if a.sweep else ()):
+            lm, _, _ = make_layers("c3", M, dev)
+            mm = time_layers(lm, steps, 5)
+            gsweep[f"M{M}"] = {"us": round(mm * 1e6, 2), "gbs": round(c3_bytes(M) / mm / 1e9, 1),
+                               "tflops": round(2.0 * M * 8192 * 8192 / mm / 1e12, 1)}
+            log(f"[bench] C3 M={M}: {gsweep[f'M{M}']}")
+            del lm
+        out["gemm_sweep"] = gsweep
         del layers
 
     g = out.get("gemv")
@@ -254,7 +291,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(g["wall"] * 1e3, 5) if g else None,
+        "ms_per_step": round(g["mean"] * 1e3, 5) if g else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -268,8 +305,9 @@ def main():
         line["pct_peak_hbm"] = round(100 * g["gbs"] / PEAK_HBM_GBS, 1)
         line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
-                            "kernel_us": round(g["mean"] * 1e6, 3), "algorithmic_bytes": g["bytes"],
-                            "back_to_back_us": round(g["b2b"] * 1e6, 3)}
+                            "kernel_us": round(g["mean"] * 1e6, 3), "algorithmic_bytes": g["bytes"]}
+        line["config1_m1"] = {"us": round(out["c1"]["us"], 2), "gbs": round(out["c1"]["gbs"], 1),
+                              "frac": round(out["c1"]["gbs"] / PEAK_HBM_GBS, 4)}
         if "sweep" in out:
             line["decode_sweep_gbs"] = out["sweep"]
     if "gemm" in out:
@@ -280,6 +318,8 @@ def main():
                                           "frac": round(gm["tflops"] / PEAK_F16_TFLOPS, 4)},
                              "config": {"workload": "C3 fused GEMM M=256: K=N=8192, fp16 x, E4M3FN, per-channel "
                                                     "UE8M0, f32 bias, fp16 out", **gm["meta"]}}
+        if out.get("gemm_sweep"):
+            line["gemm_sweep"] = out["gemm_sweep"]
     line["cpu_baseline"] = out.get("cpu")
     print(json.dumps(line), flush=True)
 
