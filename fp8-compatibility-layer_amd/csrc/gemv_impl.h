@@ -67,7 +67,7 @@ template <int MT, int XDT, int FMT, bool GROUPED, int R, int U, int TPB, bool XL
 __global__ __launch_bounds__(TPB) void gemv_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ w, const void* __restrict__ ws, int sk,
     const float* __restrict__ bias, void* __restrict__ y, int ydt, int M, int N, int K, int G, int ng,
-    int gshift, int per_block, int xlds_bytes, int slds_bytes) {
+    int gshift, int per_block, int xlds_bytes, int slds_bytes, int ldy) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int XB = XDT == TFP8_F32 ? 4 : 2;
     constexpr int GEMV_THREADS = TPB, GEMV_WAVES = TPB / 64;
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     const int items = nmine * cpr;
     const int row0 = gb * R;                                 // first row of this block
     const int rows_b = min(N, ge * R) - row0;                // rows of this block
-    float* ssc = (float*)(smem + xlds_bytes);                // block K-group scales, f32 [rows][ng]
+    float* ssc = (float*)(smem + xlds_bytes);                // block scales, f32 [rows][ng] or [rows]
     float* sout = (float*)(smem + xlds_bytes + slds_bytes);  // block results [rows][MT]
 
     const uint32_t lane16 = (uint32_t)lane * 16u;
@@ -92,24 +92,46 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     const int kx_last = min((int)last_off, K - 16);          // clamped activation index there
 
     // ---------------------------------------------------------------- load side
+    // One buffer resource spans the whole weight matrix (the host keeps N*K < 2^31); a load's
+    // scalar offset is row*K + chunk*1024. Rows past N and items past the end use offset N*K,
+    // i.e. out of range, and read zeros.
+    const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(w, (uint32_t)N * (uint32_t)K);
+    const uint32_t oob = (uint32_t)N * (uint32_t)K;
     int lt = 0, lc = 0;   // (row group ordinal, chunk) of the next item to load
     auto issue = [&](uint4 (&buf)[U][R]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool in = lt < nmine;
-            const int rg = gb + wave + GEMV_WAVES * lt;
-            const int nrows = in ? min(R, N - rg * R) : 0;
-            const __amdgpu_buffer_rsrc_t rs = buf_rsrc(w + (size_t)(in ? rg : 0) * R * K, (uint32_t)(nrows * K));
+            const int n0 = (gb + wave + GEMV_WAVES * lt) * R;
+            const uint32_t base = (uint32_t)n0 * (uint32_t)K + (uint32_t)(lc * GEMV_CHUNK);
             const uint32_t voff = lc == cpr - 1 ? voff_last : lane16;
 #pragma unroll
-            for (int r = 0; r < R; ++r) buf[u][r] = buf_load16<BUF_NT>(rs, voff, (uint32_t)(r * K + lc * GEMV_CHUNK));
+            for (int r = 0; r < R; ++r) {
+                const bool ok = lt < nmine && n0 + r < N;
+                buf[u][r] = buf_load16<BUF_NT>(wrs, voff, ok ? base + (uint32_t)(r * K) : oob);
+            }
             if (++lc == cpr) { lc = 0; ++lt; }
         }
     };
 
     uint4 sa[U][R], sb[U][R];
 
-    // Activation / scale copies that are issued before the weight prefetch (first slice only).
+    // Block-constant data staged in LDS: activations, then the scales (K-group scales of the block's
+    // rows, or their per-channel scale), then the bias. The first slice of each copy is loaded
+    // before the weight prefetch is issued and written after it, so the waits it needs never
+    // cover a weight load.
+    const int srows = max(rows_b, 0);
+    const int scount = GROUPED ? srows * ng : srows;         // f32 scale values staged
+    float* sbias = sout + per_block * R * MT;                // [rows]
+    const bool ue8 = sk == TFP8_SCALE_UE8M0;
+    const size_t s0 = GROUPED ? (size_t)row0 * ng : (size_t)row0;
+    const __amdgpu_buffer_rsrc_t srs = buf_rsrc(ws, (uint32_t)((size_t)N * ng * (ue8 ? 1 : 4)));
+    const __amdgpu_buffer_rsrc_t brs = buf_rsrc(bias, bias ? (uint32_t)(N * 4) : 0u);
+    auto scale_raw = [&](int i) -> uint32_t {
+        return ue8 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(srs, (int)(s0 + i), 0, 0)
+                   : __builtin_amdgcn_raw_buffer_load_b32(srs, (int)((s0 + i) * 4), 0, 0);
+    };
+    auto scale_f32 = [&](uint32_t raw) { return ue8 ? ue8m0_to_f32(raw) : __uint_as_float(raw); };
+
     constexpr int XC = 2;
     uint4 xcp[XC];
     const int x16n = xlds_bytes >> 4;
@@ -118,13 +140,8 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
 #pragma unroll
         for (int q = 0; q < XC; ++q) xcp[q] = buf_load16(xr, (uint32_t)(tid + q * GEMV_THREADS) * 16u, 0);
     }
-    float scp = 0.f;
-    const int scount = GROUPED ? max(rows_b, 0) * ng : 0;
-    const size_t s0 = (size_t)row0 * ng;
-    if constexpr (GROUPED) {
-        if (tid < scount)
-            scp = sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[s0 + tid]) : ((const float*)ws)[s0 + tid];
-    }
+    const uint32_t scp = tid < scount ? scale_raw(tid) : 0u;
+    const uint32_t bcp = __builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + tid) * 4, 0, 0);
 
     issue(sa);
     issue(sb);
@@ -135,12 +152,12 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
             if (tid + q * GEMV_THREADS < x16n) ((uint4*)smem)[tid + q * GEMV_THREADS] = xcp[q];
         for (int i = tid + XC * GEMV_THREADS; i < x16n; i += GEMV_THREADS) ((uint4*)smem)[i] = ((const uint4*)x)[i];
     }
-    if constexpr (GROUPED) {
-        if (tid < scount) ssc[tid] = scp;
-        for (int i = tid + GEMV_THREADS; i < scount; i += GEMV_THREADS)
-            ssc[i] = sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[s0 + i]) : ((const float*)ws)[s0 + i];
-    }
-    if constexpr (XLDS || GROUPED) __syncthreads();
+    if (tid < scount) ssc[tid] = scale_f32(scp);
+    for (int i = tid + GEMV_THREADS; i < scount; i += GEMV_THREADS) ssc[i] = scale_f32(scale_raw(i));
+    if (tid < srows) sbias[tid] = __uint_as_float(bcp);
+    for (int i = tid + GEMV_THREADS; i < srows; i += GEMV_THREADS)
+        sbias[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + i) * 4, 0, 0));
+    __syncthreads();
 
     // ---------------------------------------------------------------- compute side
     float acc[R][MT];
@@ -272,10 +289,8 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
         if (m >= M || rl >= rows_b) continue;
         const int n = row0 + rl;
         float v = sout[rl * MT + m];
-        if constexpr (!GROUPED)
-            v *= sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[n]) : ((const float*)ws)[n];
-        if (bias) v += bias[n];
-        store_elem(y, (size_t)m * N + n, ydt, v);
+        if constexpr (!GROUPED) v *= ssc[rl];
+        store_elem(y, (size_t)m * ldy + n, ydt, v + sbias[rl]);
     }
 }
 
@@ -285,7 +300,7 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
 #define TFP8_GEMV_CFG_LIST X(0, 1, 2, 32, 256) X(1, 1, 2, 64, 256) X(2, 1, 2, 64, 512) X(3, 1, 2, 64, 1024) \
     X(4, 2, 2, 32, 256) X(5, 2, 2, 32, 1024) X(6, 1, 4, 32, 1024) X(7, 4, 2, 16, 256) X(8, 2, 4, 16, 512)
 #else
-#define TFP8_GEMV_CFG_LIST X(0, 1, 2, 32, 256) X(4, 2, 2, 32, 256) X(7, 4, 2, 16, 256)
+#define TFP8_GEMV_CFG_LIST X(2, 1, 2, 64, 512) X(4, 2, 2, 32, 256) X(8, 2, 4, 16, 512)
 #endif
 
 static inline int gemv_env_int(const char* name, int dflt) {
@@ -314,14 +329,14 @@ static inline int gemv_pick(int M, int N) {
     const int forced = gemv_env_int("TFP8_GEMV_CFG", -1);
     if (forced >= 0) return forced;
     (void)N;
-    if (M <= 2) return 4;
-    if (M <= 4) return 4;
-    return 7;
+    if (M <= 1) return 4;
+    if (M <= 4) return 2;
+    return 8;
 }
 
 template <int MT, int XDT, int FMT, bool GROUPED, int R, int U, int TPB>
-static void launch_cfg(int waves_per_cu, const void* x, const uint8_t* w, const void* ws, int sk, const float* bias,
-                       void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, hipStream_t s) {
+static void launch_rows(int waves_per_cu, const void* x, const uint8_t* w, const void* ws, int sk, const float* bias,
+                        void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int ldy, hipStream_t s) {
     const int ngr = (N + R - 1) / R;
     const int wpc = gemv_env_int("TFP8_GEMV_WPC", waves_per_cu);
     const DevInfo di = dev_info();
@@ -337,16 +352,35 @@ static void launch_cfg(int waves_per_cu, const void* x, const uint8_t* w, const 
     if (per_block > max_groups) per_block = (int)max_groups;
     grid = (ngr + per_block - 1) / per_block;
     const size_t xbytes = (size_t)M * K * (XDT == TFP8_F32 ? 4 : 2);
-    const size_t sbytes = GROUPED ? ((size_t)per_block * R * ng * 4 + 15) / 16 * 16 : 0;
-    const size_t obytes = (size_t)per_block * R * MT * 4;
-    const bool xlds = xbytes + sbytes + obytes <= (size_t)di.lds;
+    const size_t sbytes = ((size_t)per_block * R * (GROUPED ? ng : 1) * 4 + 15) / 16 * 16;
+    const size_t obytes = (size_t)per_block * R * (MT + 1) * 4;   // results + bias
+    bool xlds = xbytes + sbytes + obytes <= (size_t)di.lds;
+#ifdef TFP8_GEMV_SWEEP
+    if (gemv_env_int("TFP8_GEMV_XG", 0)) xlds = false;
+#endif
     const int xl = xlds ? (int)xbytes : 0;
     if (xlds)
         gemv_kernel<MT, XDT, FMT, GROUPED, R, U, TPB, true><<<grid, TPB, xl + sbytes + obytes, s>>>(
-            x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, per_block, xl, (int)sbytes);
+            x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, per_block, xl, (int)sbytes, ldy);
     else
         gemv_kernel<MT, XDT, FMT, GROUPED, R, U, TPB, false><<<grid, TPB, sbytes + obytes, s>>>(
-            x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, per_block, 0, (int)sbytes);
+            x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, per_block, 0, (int)sbytes, ldy);
+}
+
+// Weight offsets inside a launch are 32-bit: a matrix of 2^31 bytes or more is run as several
+// launches over row ranges (output columns), each below that size.
+template <int MT, int XDT, int FMT, bool GROUPED, int R, int U, int TPB>
+static void launch_cfg(int waves_per_cu, const void* x, const uint8_t* w, const void* ws, int sk, const float* bias,
+                       void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, hipStream_t s) {
+    const long max_rows = std::max<long>(1, ((1L << 31) - 1) / K / R * R);
+    const int ysz = ydt == TFP8_F32 ? 4 : 2;
+    const int ssz = sk == TFP8_SCALE_UE8M0 ? 1 : 4;
+    for (long n0 = 0; n0 < N; n0 += max_rows) {
+        const int nr = (int)std::min<long>(max_rows, N - n0);
+        launch_rows<MT, XDT, FMT, GROUPED, R, U, TPB>(waves_per_cu, x, w + n0 * K, (const uint8_t*)ws + n0 * ng * ssz, sk,
+                                                      bias ? bias + n0 : nullptr, (uint8_t*)y + n0 * ysz, ydt, M, nr,
+                                                      K, G, ng, gshift, N, s);
+    }
 }
 
 template <int MT, int XDT, int FMT, bool GROUPED>
@@ -361,7 +395,7 @@ static void launch_m(const void* x, const uint8_t* w, const void* ws, int sk, co
     }
     TFP8_GEMV_CFG_LIST
 #undef X
-    launch_cfg<MT, XDT, FMT, GROUPED, 2, 2, 256>(32, x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, s);
+    launch_cfg<MT, XDT, FMT, GROUPED, 2, 2, 256>(32, x, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, s);  // unknown id
 }
 
 template <int XDT, int FMT, bool GROUPED>
