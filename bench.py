@@ -295,7 +295,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "C2 decode GEMV M=1: K=4096 N=14336, bf16 x, E4M3FN weights (0.1% x20 outliers), "
                                "K-group-128 f32 scales, bf16 out",

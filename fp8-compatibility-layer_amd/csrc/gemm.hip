@@ -16,6 +16,8 @@
 //     XCD (blocks go round-robin over the 8 XCDs, each with its own L2);
 //   * optional split-K over gridDim.y writes fp32 partial sums into the caller's workspace and a
 //     second kernel reduces them and applies the epilogue.
+#include <algorithm>
+
 #include "tfp8_common.h"
 
 namespace tfp8 {
@@ -276,19 +278,33 @@ GemmPlan gemm_plan(int M, int N, int K) {
     else if (forced == 5) p = {128, 128, 2, 2, 1};
     const long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     int s = 1;
-    const long part_bytes = 2L * M * N * 4;           // one slice written + read back
-    const long weight_bytes = (long)N * K;
-    while (tiles * s < 512 && s < 8 && (K / (s * 2)) >= 512 && part_bytes * (s * 2) * 5 <= weight_bytes) s *= 2;
+    // Split K until the grid covers the CUs (measured best: 4 slices for 8192^2 at M=256).
+    while (tiles * s < 256 && s < 8 && (K / (s * 2)) >= 512) s *= 2;
     const int fs = env_int("TFP8_GEMM_SPLITK", 0);
     if (fs > 0) s = fs;
     p.slices = s;
     return p;
 }
 
+size_t gemm_stream_partial_bytes(int M, int N, int K, int G, int ws_kind);
+
+// Workspace for either GEMM kernel's split-K partials (the streaming kernel's split is sized
+// with per-channel alignment, an upper bound for every group size).
 size_t gemm_partial_bytes(int M, int N, int K) {
     const GemmPlan p = gemm_plan(M, N, K);
-    return p.slices > 1 ? (size_t)p.slices * M * N * sizeof(float) : 0;
+    const size_t v1 = p.slices > 1 ? (size_t)p.slices * M * N * sizeof(float) : 0;
+    return std::max(v1, gemm_stream_partial_bytes(M, N, K, K, TFP8_SCALE_F32));
 }
+
+void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
+                          const float* bias, void* y, int ydt, hipStream_t s) {
+    const unsigned grid = grid_for((int64_t)M * N, 256);
+    splitk_reduce_kernel<<<grid, 256, 0, s>>>(part, S, M, N, ws, sk, colscale, xs, bias, y, ydt);
+}
+
+int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
+                    const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
+                    float* partial, hipStream_t s);
 
 template <typename T, int FMT, int BM, int BN, int WM, int WN>
 static void launch_gemm_cfg(const void* x, const float* xs, const uint8_t* w, const void* ws, int sk,
@@ -329,6 +345,9 @@ static int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } retu
 int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
              const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, float* partial,
              hipStream_t s) {
+    // The weight-streaming kernel takes most shapes; the LDS-tiled kernel below is the general path.
+    const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
+    if (rs != 1) return rs;
     const int ng = K / G;
     GemmPlan p = gemm_plan(M, N, K);
     int slices = p.slices, slice_len = K;
