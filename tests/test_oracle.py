@@ -10,8 +10,8 @@ Each oracle function is tied to something independent of its own code:
   dequantize_weight       exact float64 products (pow2) / one f32 rounding (non-pow2)
   activation_to_fp16      exactness invariant (test_tfp8.py:58-62) and the torch formula
   linear_ref64            a triple-loop brute force and torch float64 F.linear
-  tolerance               planted mistakes (dropped bias, transposed weight, wrong group scale)
-                          must fail it
+  tolerance               planted mistakes (dropped bias or scale, permuted K blocks, group scale
+                          off by one, wrong format, flipped sign) must fail it
 """
 import hashlib
 import math
@@ -237,6 +237,26 @@ def test_tolerance_catches_planted_mistakes():
     q_t = q.reshape(64, 8, 32)[:, ::-1, :].reshape(64, 256)   # K blocks permuted
     assert not (np.abs(O.linear_ref64(x, q_t, s, G, "e4m3fn", b) - ref) <= tol).all()
     assert not (np.abs(O.linear_ref64(x, q, s, G, "e5m2", b) - ref) <= tol).all()
+    ones = np.ones_like(s)                          # scale dropped
+    assert not (np.abs(O.linear_ref64(x, q, ones, G, "e4m3fn", b) - ref) <= tol).all()
+    q_neg = q ^ np.uint8(0x80)                      # sign bit flipped
+    assert not (np.abs(O.linear_ref64(x, q_neg, s, G, "e4m3fn", b) - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("G", [None, 32])
+def test_fake_quant_idempotent_pow2(fmt, G):
+    """dequant(quant(.)) is a projection for power-of-two scales (test_fp8_sim.py:46-60): values already
+    on the grid come back unchanged, even where the second pass picks a smaller scale."""
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((24, 128)) * 0.02).astype(np.float32)
+    w[rng.random(w.shape) < 0.01] *= 20
+    q, s, GG = O.quantize_weight(w, fmt, G, True)
+    w1 = O.dequantize_weight(q, s, fmt, GG)
+    q2, s2, _ = O.quantize_weight(w1, fmt, G, True)
+    w2 = O.dequantize_weight(q2, s2, fmt, GG)
+    assert np.array_equal(w1, w2)
+    assert not np.array_equal(w1, w)
 
 
 def test_cpu_path_matches_oracle():
