@@ -2,13 +2,15 @@
 //
 // y[m,n] = xs[m] * sum_g s(n,g) * sum_{k in g} x[m,k] * decode(w[n,k]) + bias[n]
 // (reference gemm_w8a16, tfp8/csrc/tfp8_kernels.cu:271-411), built for CDNA4:
-//   * block tile BM x BN x 64, 4 waves in a WM x WN grid, wave tile (BM/WM) x (BN/WN) made of
-//     16x16 outputs of v_mfma_f32_16x16x32_{f16,bf16} (fp32 accumulation);
-//   * per 64-wide K step the activation tile (f16/bf16) and the raw FP8 weight tile (1 byte per
-//     element, half the LDS footprint of a decoded tile) are staged through registers into a
-//     double-buffered LDS pair; each wave reads its 8-byte B fragments from LDS and decodes
-//     them in registers with v_cvt_scalef32_pk_{f16,bf16}_{fp8,bf8} right before the MFMA, so
-//     the weight is never written back decoded, to LDS or to HBM;
+//   * block tile BM x BN x BK, WM x WN waves (8 for the large tiles: two waves per SIMD keep the
+//     matrix cores fed, one cannot), wave tile (BM/WM) x (BN/WN) made of 16x16 outputs of
+//     v_mfma_f32_16x16x32_{f16,bf16} (fp32 accumulation);
+//   * per K tile the activation tile (f16/bf16) and the raw FP8 weight tile (1 byte per element,
+//     half the LDS footprint of a decoded tile) are loaded with unconditional buffer loads
+//     (rows past M/N and k past the slice read zeros) two tiles ahead into registers, then
+//     written to a double-buffered LDS pair; each wave reads its 8-byte B fragments from LDS
+//     and decodes them in registers with v_cvt_scalef32_pk_{f16,bf16}_{fp8,bf8} right before
+//     the MFMA, so the weight is never written back decoded, to LDS or to HBM;
 //   * per-channel scales (one group) are applied in the epilogue; K-group scales (G % 32 == 0)
 //     multiply an fp32 partial accumulator at every group boundary (exact for any f32 scale,
 //     no folding of scales into 16-bit weights);
@@ -22,9 +24,8 @@
 
 namespace tfp8 {
 
-constexpr int GEMM_BK = 64;
-constexpr int A_ROW_BYTES = GEMM_BK * 2 + 16;   // 144: 16-byte pad keeps ds_read_b128 conflict-free
-constexpr int B_ROW_BYTES = GEMM_BK + 16;       // 80
+constexpr uint32_t GEMM_BUF_FLAGS = 0x00020000u;   // buffer resource word 3 (raw, 32-bit format)
+constexpr uint32_t GEMM_OOB = 0x80000000u;         // a byte offset past every resource used here
 
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<_Float16> {
@@ -57,7 +58,11 @@ __device__ __forceinline__ float scale_at(const void* ws, int sk, size_t i) {
     return sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[i]) : ((const float*)ws)[i];
 }
 
-template <typename T, int FMT, int BM, int BN, int WM, int WN, bool GROUPED>
+__device__ __forceinline__ uint4 gload16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));
+}
+
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int BK, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const T* __restrict__ x, const float* __restrict__ xs, const uint8_t* __restrict__ w,
     const void* __restrict__ ws, int sk, const float* __restrict__ bias, void* __restrict__ y, int ydt,
@@ -68,15 +73,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 16, TN = WTN / 16;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 16x16 MFMA tile");
-    constexpr int A_CHUNKS = BM * (GEMM_BK / 8);    // 16-byte chunks of the activation tile
-    constexpr int B_CHUNKS = BN * (GEMM_BK / 16);   // 16-byte chunks of the FP8 weight tile
+    static_assert(BK % 32 == 0, "K tile is whole MFMA steps");
+    constexpr int AROW = BK * 2 + 16;               // 16-byte row pad: conflict-free ds_read_b128
+    constexpr int BROW = BK + 16;
+    constexpr int A_CPR = BK / 8, B_CPR = BK / 16;  // 16-byte chunks per tile row
+    constexpr int A_CHUNKS = BM * A_CPR, B_CHUNKS = BN * B_CPR;
     constexpr int CA = (A_CHUNKS + NT - 1) / NT;
     constexpr int CB = (B_CHUNKS + NT - 1) / NT;
 
-    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * A_ROW_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * B_ROW_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * AROW];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * BROW];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
     // XCD-aware tile order: consecutive ids land on one XCD, and consecutive ids walk M first,
@@ -89,35 +98,59 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const int kbeg = blockIdx.y * slice_len;
     const int kend = min(K, kbeg + slice_len);
 
-    uint4 ra[CA], rb[CB];
-    auto load_tile = [&](int kt) {
+    // One buffer resource per operand over this block's rows: rows past M / N are out of range
+    // and read as zeros, so every load below is unconditional.
+    const __amdgpu_buffer_rsrc_t ra_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(x + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * (uint32_t)K * 2u), (int)GEMM_BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t rb_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(w + (size_t)n0 * K), (short)0, (int)((uint32_t)min(BN, N - n0) * (uint32_t)K), (int)GEMM_BUF_FLAGS);
+
+    // Per-lane chunk coordinates (fixed over the K loop).
+    uint32_t a_row_off[CA], b_row_off[CB];
+    int a_col[CA], b_col[CB];
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+        const int c = tid + i * NT;
+        const int row = c / A_CPR;
+        a_col[i] = (c % A_CPR) * 8;
+        a_row_off[i] = c < A_CHUNKS ? (uint32_t)row * (uint32_t)K * 2u : GEMM_OOB;
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * NT;
+        const int row = c / B_CPR;
+        b_col[i] = (c % B_CPR) * 16;
+        b_row_off[i] = c < B_CHUNKS ? (uint32_t)row * (uint32_t)K : GEMM_OOB;
+    }
+
+    uint4 ra[2][CA], rb[2][CB];
+    // Global -> registers for the K tile at kt (k >= kend reads zeros).
+    auto issue = [&](int slot, int kt) {
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
-            const int c = tid + i * NT;
-            const int row = c >> 3, col = (c & 7) * 8;
-            const int gm = m0 + row, gk = kt + col;
-            ra[i] = (c < A_CHUNKS && gm < M && gk < kend) ? *(const uint4*)(x + (size_t)gm * K + gk)
-                                                          : make_uint4(0, 0, 0, 0);
+            const int gk = kt + a_col[i];
+            const uint32_t off = gk < kend ? a_row_off[i] + (uint32_t)gk * 2u : GEMM_OOB;
+            ra[slot][i] = gload16(ra_rsrc, off);
         }
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
-            const int c = tid + i * NT;
-            const int row = c >> 2, col = (c & 3) * 16;
-            const int gn = n0 + row, gk = kt + col;
-            rb[i] = (c < B_CHUNKS && gn < N && gk < kend) ? *(const uint4*)(w + (size_t)gn * K + gk)
-                                                          : make_uint4(0, 0, 0, 0);
+            const int gk = kt + b_col[i];
+            const uint32_t off = gk < kend ? b_row_off[i] + (uint32_t)gk : GEMM_OOB;
+            rb[slot][i] = gload16(rb_rsrc, off);
         }
     };
-    auto store_tile = [&](int buf) {
+    auto commit = [&](int slot, int buf) {
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
             const int c = tid + i * NT;
-            if (c < A_CHUNKS) *(uint4*)&sA[buf][(c >> 3) * A_ROW_BYTES + (c & 7) * 16] = ra[i];
+            if (A_CHUNKS % NT == 0 || c < A_CHUNKS)
+                *(uint4*)&sA[buf][(c / A_CPR) * AROW + (c % A_CPR) * 16] = ra[slot][i];
         }
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
             const int c = tid + i * NT;
-            if (c < B_CHUNKS) *(uint4*)&sB[buf][(c >> 2) * B_ROW_BYTES + (c & 3) * 16] = rb[i];
+            if (B_CHUNKS % NT == 0 || c < B_CHUNKS)
+                *(uint4*)&sB[buf][(c / B_CPR) * BROW + (c % B_CPR) * 16] = rb[slot][i];
         }
     };
 
@@ -152,54 +185,117 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const int brow = wn * WTN + (lane & 15);
     const int kq = 8 * (lane >> 4);   // this lane's 8-wide K slot inside a 32-wide MFMA step
 
-    load_tile(kbeg);
-    store_tile(0);
-    __syncthreads();
-
-    int buf = 0;
-    for (int kt = kbeg; kt < kend; kt += GEMM_BK) {
-        const bool more = kt + GEMM_BK < kend;
-        if (more) load_tile(kt + GEMM_BK);
+    // One K tile from LDS buffer `buf`.  The fragments of MFMA step ks+1 are read while step ks
+    // multiplies, and the B operands of step ks+1 are decoded between the MFMAs of step ks
+    // (one conversion in each MFMA's shadow), so neither LDS latency nor the decode leaves the
+    // matrix core idle; the two waves of a SIMD run in phase after each barrier, so the
+    // interleave has to happen inside the wave.
+    auto compute = [&](int buf, int kt) {
+        uint2 braw[2][TN];
+        V araw[2][TM];
+        V bf[2][TN];
+        auto fetch = [&](int slot, int ks) {
 #pragma unroll
-        for (int ks = 0; ks < GEMM_BK / 32; ++ks) {
+            for (int b = 0; b < TN; ++b)
+                braw[slot][b] = *(const uint2*)&sB[buf][(brow + b * 16) * BROW + ks * 32 + kq];
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                araw[slot][a] = *(const V*)&sA[buf][(arow + a * 16) * AROW + (ks * 32 + kq) * 2];
+        };
+        auto decode = [&](int slot) {
+#pragma unroll
+            for (int b = 0; b < TN; ++b) bf[slot][b] = decode_frag<T, FMT>(braw[slot][b]);
+        };
+        fetch(0, 0);
+        if (BK / 32 > 1) fetch(1, 1);
+        decode(0);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int cur = ks & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            // Steps past the slice end multiply the zeros their loads returned, so no step needs
+            // a guard; an extra fold there adds prt = 0 (or NaN where a non-finite scale already
+            // makes the column NaN).
             const int kk = kt + ks * 32;
-            if (kk < kend) {
-                V af[TM], bf[TN];
+            // MFMAs of this step in program order, each followed by its share of the next step's
+            // conversions (none after the first two: their LDS reads may still be in flight);
+            // sched_barrier(0) after each pair keeps the order.
+            constexpr int NM = TM * TN, NC = 4 * TN;
+            constexpr int LEAD = NM > 2 ? 2 : 0;
+            constexpr int PER = NM > LEAD ? (NC + NM - LEAD - 1) / (NM - LEAD) : NC;
+            const bool dec = ks + 1 < BK / 32;
+            uint32_t nb[TN][4];
 #pragma unroll
-                for (int a = 0; a < TM; ++a)
-                    af[a] = *(const V*)&sA[buf][(arow + a * 16) * A_ROW_BYTES + (ks * 32 + kq) * 2];
+            for (int i = 0; i < NM; ++i) {
+                const int a = i / TN, b = i % TN;
+                if constexpr (GROUPED) prt[a][b] = Op::run(araw[cur][a], bf[cur][b], prt[a][b]);
+                else acc[a][b] = Op::run(araw[cur][a], bf[cur][b], acc[a][b]);
+                if (dec && i >= LEAD) {
 #pragma unroll
-                for (int b = 0; b < TN; ++b)
-                    bf[b] = decode_frag<T, FMT>(*(const uint2*)&sB[buf][(brow + b * 16) * B_ROW_BYTES + ks * 32 + kq]);
-#pragma unroll
-                for (int a = 0; a < TM; ++a)
-#pragma unroll
-                    for (int b = 0; b < TN; ++b) {
-                        if constexpr (GROUPED) prt[a][b] = Op::run(af[a], bf[b], prt[a][b]);
-                        else acc[a][b] = Op::run(af[a], bf[b], acc[a][b]);
+                    for (int j = (i - LEAD) * PER; j < (i - LEAD + 1) * PER && j < NC; ++j) {
+                        const int fb = j / 4, wd = j % 4;
+                        const uint32_t src = (wd < 2) ? braw[cur ^ 1][fb].x : braw[cur ^ 1][fb].y;
+                        nb[fb][wd] = Op::template cvt<FMT>(src, (wd & 1) != 0);
                     }
-                if constexpr (GROUPED) {
-                    if (kk + 32 == gnext || kk + 32 >= kend) {
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (dec) {
 #pragma unroll
-                        for (int a = 0; a < TM; ++a)
+                for (int fb = 0; fb < TN; ++fb)
+                    bf[cur ^ 1][fb] = __builtin_bit_cast(V, make_uint4(nb[fb][0], nb[fb][1], nb[fb][2], nb[fb][3]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + 2 < BK / 32) fetch(cur, ks + 2);   // this step's slot is free again
+            if constexpr (GROUPED) {
+                if (kk + 32 == gnext || kk + 32 >= kend) {
 #pragma unroll
-                            for (int b = 0; b < TN; ++b) {
+                    for (int a = 0; a < TM; ++a)
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) acc[a][b][i] = fmaf(prt[a][b][i], gs[b], acc[a][b][i]);
-                                prt[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-                            }
-                        gidx = min(gidx + 1, ng - 1);
-                        gnext += G;
+                        for (int b = 0; b < TN; ++b) {
 #pragma unroll
-                        for (int b = 0; b < TN; ++b) gs[b] = scale_at(ws, sk, (size_t)colc[b] * ng + gidx);
-                    }
+                            for (int i = 0; i < 4; ++i) acc[a][b][i] = fmaf(prt[a][b][i], gs[b], acc[a][b][i]);
+                            prt[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        }
+                    gidx = min(gidx + 1, ng - 1);
+                    gnext += G;
+#pragma unroll
+                    for (int b = 0; b < TN; ++b) gs[b] = scale_at(ws, sk, (size_t)colc[b] * ng + gidx);
                 }
             }
         }
-        if (more) store_tile(buf ^ 1);
+    };
+
+    // Pipeline: LDS double buffer, and the global loads of a tile are issued two tiles ahead of
+    // its use (register slots 0/1), so one full tile of MFMA work covers each load's latency.
+    // Loads past the slice's end read zeros and are never consumed.
+    // The loop runs whole pairs of tiles and an odd last tile is handled after it: a break in
+    // the middle of the pair would merge a path with slot-0 loads still in flight into the
+    // loop head, and the compiler would then drain every load there on every iteration.
+    const int ntiles = (kend - kbeg + BK - 1) / BK;
+    issue(0, kbeg);
+    issue(1, kbeg + BK);
+    commit(0, 0);
+    __syncthreads();
+    // sched_barrier(0) keeps each phase in place: otherwise the scheduler hoists the LDS writes
+    // of the other buffer above the MFMA work (nothing orders them), which makes the wave wait
+    // for the newest loads at the top of every half-iteration.
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+        issue(0, kbeg + (t + 2) * BK);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0, kbeg + t * BK);
+        __builtin_amdgcn_sched_barrier(0);
+        commit(1, 1);
         __syncthreads();
-        buf ^= 1;
+        issue(1, kbeg + (t + 3) * BK);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1, kbeg + (t + 1) * BK);
+        __builtin_amdgcn_sched_barrier(0);
+        commit(0, 0);
+        __syncthreads();
     }
+    if (t < ntiles) compute(0, kbeg + t * BK);
 
     // Epilogue.  MFMA 16x16 output layout: lane l holds rows 4*(l>>4)+i, column l&15.
     const int rbase = m0 + wm * WTM + 4 * (lane >> 4);
@@ -233,7 +329,63 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     }
 }
 
-// Split-K epilogue: y = (sum_s part[s]) * colscale * xs + bias.
+// Split-K epilogue: y = (sum_s part[s]) * colscale * xs + bias, slices added in order.
+// Fast form: 8 consecutive columns per thread, every slice's loads issued before the first add,
+// one 16-byte store per thread (N % 8 == 0, y 16-byte aligned, at most 8 slices); generic form:
+// one column per thread.
+template <int YDT, int SK>
+__global__ __launch_bounds__(256) void splitk_reduce8_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                             const void* __restrict__ ws, int colscale,
+                                                             const float* __restrict__ xs,
+                                                             const float* __restrict__ bias, void* __restrict__ y) {
+    const int64_t total = (int64_t)M * N;
+    const int nv = N / 8;
+    const int64_t items = (int64_t)M * nv;
+    for (int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x; it < items; it += (int64_t)gridDim.x * 256) {
+        const int row = (int)(it / nv), col = (int)(it - (int64_t)row * nv) * 8;
+        const size_t i = (size_t)row * N + col;
+        float4 lo[8], hi[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            if (s < S) {
+                lo[s] = *(const float4*)(part + (size_t)s * total + i);
+                hi[s] = *(const float4*)(part + (size_t)s * total + i + 4);
+            }
+        float v[8] = {lo[0].x, lo[0].y, lo[0].z, lo[0].w, hi[0].x, hi[0].y, hi[0].z, hi[0].w};
+#pragma unroll
+        for (int s = 1; s < 8; ++s)
+            if (s < S) {
+                v[0] += lo[s].x; v[1] += lo[s].y; v[2] += lo[s].z; v[3] += lo[s].w;
+                v[4] += hi[s].x; v[5] += hi[s].y; v[6] += hi[s].z; v[7] += hi[s].w;
+            }
+        if (colscale) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] *= load_scale<SK>(ws, (size_t)col + j);
+        }
+        float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bv[j] = bias[col + j];
+        }
+        const float xr = xs ? xs[row] : 1.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = xs ? fmaf(v[j], xr, bv[j]) : v[j] + bv[j];
+        if constexpr (YDT == TFP8_F32) {
+            *(float4*)((float*)y + i) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)((float*)y + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t l = YDT == TFP8_BF16 ? f32_to_bf16_bits(v[2 * j]) : f32_to_f16_bits(v[2 * j]);
+                const uint32_t h = YDT == TFP8_BF16 ? f32_to_bf16_bits(v[2 * j + 1]) : f32_to_f16_bits(v[2 * j + 1]);
+                w[j] = l | (h << 16);
+            }
+            *(uint4*)((uint16_t*)y + i) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                                             const void* __restrict__ ws, int sk, int colscale,
                                                             const float* __restrict__ xs,
@@ -241,9 +393,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                             int ydt) {
     const int64_t total = (int64_t)M * N;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        float v = 0.f;
-        for (int s = 0; s < S; ++s) v += part[(size_t)s * total + i];
         const int row = (int)(i / N), col = (int)(i % N);
+        float v = part[i];
+        for (int s = 1; s < S; ++s) v += part[(size_t)s * total + i];
         if (colscale) v *= scale_at(ws, sk, (size_t)col);
         const float bv = bias ? bias[col] : 0.f;
         store_elem(y, (size_t)i, ydt, xs ? fmaf(v, xs[row], bv) : v + bv);
@@ -252,8 +404,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 // ------------------------------------------------------------------ planning
 struct GemmPlan {
-    int bm, bn, wm, wn;   // tile config
-    int slices;           // split-K factor (1 = none)
+    int bm, bn, wm, wn, bk;   // tile config
+    int slices;               // split-K factor (1 = none)
 };
 
 static int env_int(const char* name, int dflt) {
@@ -261,27 +413,34 @@ static int env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-// Tile config by M; split K when the tile grid would leave CUs idle and the fp32 partials stay
-// small next to the weight stream.
-GemmPlan gemm_plan(int M, int N, int K) {
+static const GemmPlan GEMM_CFGS[] = {
+    {0, 0, 0, 0, 0, 1},
+    {16, 64, 1, 4, 64, 1},  {32, 64, 2, 2, 64, 1},   {64, 64, 2, 2, 64, 1},    {64, 128, 2, 2, 64, 1},
+    {128, 128, 2, 2, 64, 1}, {128, 128, 4, 2, 64, 1}, {128, 128, 2, 4, 64, 1},  {256, 128, 4, 2, 64, 1},
+    {128, 64, 4, 2, 64, 1}, {128, 128, 2, 4, 128, 1}, {128, 128, 4, 2, 128, 1}, {128, 256, 2, 4, 64, 1},
+    {128, 256, 2, 4, 128, 1},
+};
+constexpr int GEMM_NCFG = (int)(sizeof(GEMM_CFGS) / sizeof(GEMM_CFGS[0]));
+
+// Tile config by M (sweep on MI355X, K = N = 8192): above 128 rows the 128 x 256 tile with
+// 128-wide K steps (8 waves, 2 per SIMD), or 128 x 128 with K-group scales, whose extra fp32
+// partial accumulators would spill the larger tile.  Split K until the grid has a block per CU
+// (two for the 4-wave tiles), keeping slices long next to the fp32 partials they produce.
+GemmPlan gemm_plan(int M, int N, int K, bool grouped) {
     GemmPlan p;
-    if (M <= 16) p = {16, 64, 1, 4, 1};
-    else if (M <= 32) p = {32, 64, 2, 2, 1};
-    else if (M <= 64) p = {64, 64, 2, 2, 1};
-    else if (M <= 128) p = {64, 128, 2, 2, 1};
-    else p = {128, 128, 2, 2, 1};
-    const int forced = env_int("TFP8_GEMM_TILE", 0);   // tuning hook: 1..5 picks a config above
-    if (forced == 1) p = {16, 64, 1, 4, 1};
-    else if (forced == 2) p = {32, 64, 2, 2, 1};
-    else if (forced == 3) p = {64, 64, 2, 2, 1};
-    else if (forced == 4) p = {64, 128, 2, 2, 1};
-    else if (forced == 5) p = {128, 128, 2, 2, 1};
+    if (M <= 16) p = GEMM_CFGS[1];
+    else if (M <= 32) p = GEMM_CFGS[2];
+    else if (M <= 64) p = GEMM_CFGS[3];
+    else if (M <= 128) p = GEMM_CFGS[4];
+    else p = grouped ? GEMM_CFGS[7] : GEMM_CFGS[13];
+    const int forced = env_int("TFP8_GEMM_TILE", 0);   // tuning hook: index into GEMM_CFGS
+    if (forced > 0 && forced < GEMM_NCFG) p = GEMM_CFGS[forced];
     const long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+    const long want = p.wm * p.wn == 8 ? 256 : 512;
     int s = 1;
-    // Split K until the grid covers the CUs (measured best: 4 slices for 8192^2 at M=256).
-    while (tiles * s < 256 && s < 8 && (K / (s * 2)) >= 512) s *= 2;
+    while (tiles * s < want && s < 8 && (K / (s * 2)) >= 1024) s *= 2;
     const int fs = env_int("TFP8_GEMM_SPLITK", 0);
-    if (fs > 0) s = fs;
+    if (fs > 0) s = std::min(fs, 8);
     p.slices = s;
     return p;
 }
@@ -291,32 +450,48 @@ size_t gemm_stream_partial_bytes(int M, int N, int K, int G, int ws_kind);
 // Workspace for either GEMM kernel's split-K partials (the streaming kernel's split is sized
 // with per-channel alignment, an upper bound for every group size).
 size_t gemm_partial_bytes(int M, int N, int K) {
-    const GemmPlan p = gemm_plan(M, N, K);
-    const size_t v1 = p.slices > 1 ? (size_t)p.slices * M * N * sizeof(float) : 0;
+    const GemmPlan p = gemm_plan(M, N, K, false), q = gemm_plan(M, N, K, true);
+    const int sl = std::max(p.slices, q.slices);
+    const size_t v1 = sl > 1 ? (size_t)sl * M * N * sizeof(float) : 0;
     return std::max(v1, gemm_stream_partial_bytes(M, N, K, K, TFP8_SCALE_F32));
 }
 
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
                           const float* bias, void* y, int ydt, hipStream_t s) {
-    const unsigned grid = grid_for((int64_t)M * N, 256);
-    splitk_reduce_kernel<<<grid, 256, 0, s>>>(part, S, M, N, ws, sk, colscale, xs, bias, y, ydt);
+    if (N % 8 == 0 && S <= 8 && (uintptr_t)y % 16 == 0) {
+        const unsigned grid = grid_for((int64_t)M * N / 8, 256);
+#define TFP8_RED(YD, SKV) splitk_reduce8_kernel<YD, SKV><<<grid, 256, 0, s>>>(part, S, M, N, ws, colscale, xs, bias, y)
+        if (sk == TFP8_SCALE_UE8M0) {
+            if (ydt == TFP8_F32) TFP8_RED(TFP8_F32, TFP8_SCALE_UE8M0);
+            else if (ydt == TFP8_BF16) TFP8_RED(TFP8_BF16, TFP8_SCALE_UE8M0);
+            else TFP8_RED(TFP8_F16, TFP8_SCALE_UE8M0);
+        } else {
+            if (ydt == TFP8_F32) TFP8_RED(TFP8_F32, TFP8_SCALE_F32);
+            else if (ydt == TFP8_BF16) TFP8_RED(TFP8_BF16, TFP8_SCALE_F32);
+            else TFP8_RED(TFP8_F16, TFP8_SCALE_F32);
+        }
+#undef TFP8_RED
+    } else {
+        splitk_reduce_kernel<<<grid_for((int64_t)M * N, 256), 256, 0, s>>>(part, S, M, N, ws, sk, colscale, xs, bias, y,
+                                                                          ydt);
+    }
 }
 
 int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
                     const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
                     float* partial, hipStream_t s);
 
-template <typename T, int FMT, int BM, int BN, int WM, int WN>
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int BK>
 static void launch_gemm_cfg(const void* x, const float* xs, const uint8_t* w, const void* ws, int sk,
                             const float* bias, void* y, int ydt, int M, int N, int K, int G, int ng, float* part,
                             int slices, int slice_len, hipStream_t s) {
     const int nt = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     dim3 grid(nt, slices);
     if (ng > 1)
-        gemm_kernel<T, FMT, BM, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, s>>>(
+        gemm_kernel<T, FMT, BM, BN, WM, WN, BK, true><<<grid, 64 * WM * WN, 0, s>>>(
             (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, part, slice_len);
     else
-        gemm_kernel<T, FMT, BM, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, s>>>(
+        gemm_kernel<T, FMT, BM, BN, WM, WN, BK, false><<<grid, 64 * WM * WN, 0, s>>>(
             (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, part, slice_len);
 }
 
@@ -324,17 +499,25 @@ template <typename T, int FMT>
 static void launch_gemm_t(const GemmPlan& p, const void* x, const float* xs, const uint8_t* w, const void* ws,
                           int sk, const float* bias, void* y, int ydt, int M, int N, int K, int G, int ng,
                           float* part, int slices, int slice_len, hipStream_t s) {
-#define TFP8_GEMM_CFG(BM_, BN_, WM_, WN_)                                                                    \
-    if (p.bm == BM_ && p.bn == BN_ && p.wm == WM_ && p.wn == WN_) {                                         \
-        launch_gemm_cfg<T, FMT, BM_, BN_, WM_, WN_>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, part,     \
-                                                    slices, slice_len, s);                                  \
+#define TFP8_GEMM_CFG(BM_, BN_, WM_, WN_, BK_)                                                               \
+    if (p.bm == BM_ && p.bn == BN_ && p.wm == WM_ && p.wn == WN_ && p.bk == BK_) {                            \
+        launch_gemm_cfg<T, FMT, BM_, BN_, WM_, WN_, BK_>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, part, \
+                                                         slices, slice_len, s);                              \
         return;                                                                                             \
     }
-    TFP8_GEMM_CFG(16, 64, 1, 4)
-    TFP8_GEMM_CFG(32, 64, 2, 2)
-    TFP8_GEMM_CFG(64, 64, 2, 2)
-    TFP8_GEMM_CFG(64, 128, 2, 2)
-    TFP8_GEMM_CFG(128, 128, 2, 2)
+    TFP8_GEMM_CFG(16, 64, 1, 4, 64)
+    TFP8_GEMM_CFG(32, 64, 2, 2, 64)
+    TFP8_GEMM_CFG(64, 64, 2, 2, 64)
+    TFP8_GEMM_CFG(64, 128, 2, 2, 64)
+    TFP8_GEMM_CFG(128, 128, 2, 2, 64)
+    TFP8_GEMM_CFG(128, 128, 4, 2, 64)
+    TFP8_GEMM_CFG(128, 128, 2, 4, 64)
+    TFP8_GEMM_CFG(256, 128, 4, 2, 64)
+    TFP8_GEMM_CFG(128, 64, 4, 2, 64)
+    TFP8_GEMM_CFG(128, 128, 2, 4, 128)
+    TFP8_GEMM_CFG(128, 128, 4, 2, 128)
+    TFP8_GEMM_CFG(128, 256, 2, 4, 64)
+    TFP8_GEMM_CFG(128, 256, 2, 4, 128)
 #undef TFP8_GEMM_CFG
 }
 
@@ -349,12 +532,12 @@ int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, cons
     const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
     if (rs != 1) return rs;
     const int ng = K / G;
-    GemmPlan p = gemm_plan(M, N, K);
+    GemmPlan p = gemm_plan(M, N, K, ng > 1);
     int slices = p.slices, slice_len = K;
     if (slices > 1) {
-        // Slices are whole 64-wide K tiles, and whole K groups when the scales are grouped.
-        int align = GEMM_BK;
-        if (ng > 1) align = GEMM_BK / gcd_i(GEMM_BK, G) * G;
+        // Slices are whole K tiles, and whole K groups when the scales are grouped.
+        int align = p.bk;
+        if (ng > 1) align = p.bk / gcd_i(p.bk, G) * G;
         slice_len = ((K + slices - 1) / slices + align - 1) / align * align;
         slices = (K + slice_len - 1) / slice_len;
         if (slices <= 1) { slices = 1; slice_len = K; }
@@ -369,9 +552,7 @@ int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, cons
     }
     int rc = check_launch("tfp8_gemm");
     if (rc || slices <= 1) return rc;
-    const unsigned grid = grid_for((int64_t)M * N, 256);
-    splitk_reduce_kernel<<<grid, 256, 0, s>>>(part, slices, M, N, ws, ws_kind, ng == 1 ? 1 : 0, xs, bias, y,
-                                              y_dtype);
+    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, ng == 1 ? 1 : 0, xs, bias, y, y_dtype, s);
     return check_launch("tfp8_gemm splitk reduce");
 }
 

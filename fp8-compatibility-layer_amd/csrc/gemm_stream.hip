@@ -294,9 +294,9 @@ void gemm_stream_plan(int M, int N, int K, int G, int gmode, int* tm, int* nw, i
     if (gmode == GM_F32) { int a = KC, b = G; while (b) { int t = a % b; a = b; b = t; } align = KC / a * G; }
     int s = 1;
     const int want = 2 * gs_cus();
-    while (ntile * s * 2 <= want && (K / (s * 2)) >= 2 * KC) s *= 2;
+    while (ntile * s * 2 <= want && s < 8 && (K / (s * 2)) >= 2 * KC) s *= 2;
     const int fs = gs_env_int("TFP8_GS_SPLITK", 0);
-    if (fs > 0) s = fs;
+    if (fs > 0) s = std::min(fs, 8);
     int len = ((K + s - 1) / s + align - 1) / align * align;
     s = (K + len - 1) / len;
     *tm = T; *nw = NWv; *kcs = KCSv; *slices = s; *slice_len = len;

@@ -288,3 +288,17 @@ def test_config4_e5m2_block32_ue8m0():
     t = torch.tensor([1e9, -1e9, float("inf"), -float("inf"), 2.0 ** -16, -(2.0 ** -15), 3 * 2.0 ** -16, 0.0, -0.0])
     from tfp8.formats import encode
     assert torch.equal(encode(t.cuda(), "e5m2").cpu(), torch.from_numpy(O.encode(t.numpy(), "e5m2")))
+
+
+@pytest.mark.parametrize("tile", list(range(1, 14)))
+def test_tiled_gemm_every_config(tile, monkeypatch):
+    """Every LDS-tiled GEMM configuration (forced through the library's tuning hooks), with and
+    without split-K, on ragged shapes: rows past M and N, a K tail that is not a whole K tile,
+    per-channel and K-group (f32 G=32, UE8M0 G=64) scales, f16 and bf16 activations."""
+    monkeypatch.setenv("TFP8_GEMM_V1", "1")
+    monkeypatch.setenv("TFP8_GEMM_TILE", str(tile))
+    for split in (1, 3):
+        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+        _run(40, 200, 1120, None, torch.float16, xdt=torch.float16, seed=tile)
+        _run(130, 72, 640, 32, torch.bfloat16, xdt=torch.bfloat16, seed=tile + 1)
+        _run(257, 136, 704, 64, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", seed=tile + 2)
