@@ -1,0 +1,244 @@
+"""Llama-style decoder on the FP8 W8A16 path versus native bf16 (reference tfp8/examples/demo_llm.py).
+
+    python -m tfp8.examples.demo_llm --size c5      # 8 layers, d=2048, 16 heads, FFN 5632, vocab 32000
+    python -m tfp8.examples.demo_llm --size tiny    # 2 layers, seconds
+
+The model is built here (random N(0, 0.02) init, tied embedding / output head), converted with
+prepare_model(profile="llm_safe"), and measured the way the reference demo measures it: logits
+agreement with the bf16 model (cosine, relative L2, top-1), prefill and per-token decode latency,
+and the FP8Linear path counters.  Layout choices for the GPU:
+  * the KV cache is preallocated [B, heads, max_len, head_dim] and written in place;
+  * attention runs in fp32 on contiguous operands (scores, causal mask, softmax, values);
+  * the tied output head keeps one fp32 copy of the embedding (the reference re-widens the
+    embedding to fp32 on every call, demo_llm.py:127).
+"""
+import argparse
+import math
+import statistics
+import time
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+SIZES = {
+    "tiny": dict(dim=1024, n_layers=2, n_heads=8, n_kv=8, ffn=2816, vocab=8192),
+    "c5": dict(dim=2048, n_layers=8, n_heads=16, n_kv=16, ffn=5632, vocab=32000),
+}
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, d, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        inv = torch.rsqrt(xf.square().mean(-1, keepdim=True) + self.eps)
+        return (xf * inv * self.weight.float()).to(x.dtype)
+
+
+def _rotary(x, cos, sin):
+    """Rotate the two halves of the head dimension: x = [x1, x2] -> [x1 c - x2 s, x2 c + x1 s]."""
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h].float(), x[..., h:].float()
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1).to(x.dtype)
+
+
+class Attention(nn.Module):
+    def __init__(self, c):
+        super().__init__()
+        self.nh, self.nkv = c["n_heads"], c["n_kv"]
+        self.hd = c["dim"] // c["n_heads"]
+        d = c["dim"]
+        self.q_proj = nn.Linear(d, self.nh * self.hd, bias=False)
+        self.k_proj = nn.Linear(d, self.nkv * self.hd, bias=False)
+        self.v_proj = nn.Linear(d, self.nkv * self.hd, bias=False)
+        self.o_proj = nn.Linear(self.nh * self.hd, d, bias=False)
+
+    def forward(self, x, cos, sin, cache, start):
+        B, T, _ = x.shape
+        q = _rotary(self.q_proj(x).view(B, T, self.nh, self.hd), cos, sin)
+        k = _rotary(self.k_proj(x).view(B, T, self.nkv, self.hd), cos, sin)
+        v = self.v_proj(x).view(B, T, self.nkv, self.hd)
+        kc, vc = cache
+        kc[:, :, start:start + T] = k.transpose(1, 2)
+        vc[:, :, start:start + T] = v.transpose(1, 2)
+        L = start + T
+        rep = self.nh // self.nkv
+        keys = kc[:, :, :L].float()
+        vals = vc[:, :, :L].float()
+        if rep > 1:
+            keys, vals = keys.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
+        qf = q.transpose(1, 2).float().contiguous()                          # [B, H, T, hd]
+        scores = torch.matmul(qf, keys.transpose(-1, -2).contiguous()) / math.sqrt(self.hd)
+        if T > 1:
+            qpos = torch.arange(start, L, device=x.device)[:, None]
+            kpos = torch.arange(L, device=x.device)[None, :]
+            scores = scores.masked_fill(kpos > qpos, float("-inf"))
+        o = torch.matmul(torch.softmax(scores, -1), vals.contiguous())           # [B, H, T, hd]
+        return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
+
+
+class MLP(nn.Module):
+    def __init__(self, c):
+        super().__init__()
+        self.gate_proj = nn.Linear(c["dim"], c["ffn"], bias=False)
+        self.up_proj = nn.Linear(c["dim"], c["ffn"], bias=False)
+        self.down_proj = nn.Linear(c["ffn"], c["dim"], bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, c):
+        super().__init__()
+        self.input_layernorm = RMSNorm(c["dim"])
+        self.self_attn = Attention(c)
+        self.post_attention_layernorm = RMSNorm(c["dim"])
+        self.mlp = MLP(c)
+
+    def forward(self, x, cos, sin, cache, start):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin, cache, start)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class Llama(nn.Module):
+    def __init__(self, c):
+        super().__init__()
+        self.c = c
+        self.embed = nn.Embedding(c["vocab"], c["dim"])
+        self.layers = nn.ModuleList(Block(c) for _ in range(c["n_layers"]))
+        self.norm = RMSNorm(c["dim"])
+        self.lm_head = nn.Linear(c["dim"], c["vocab"], bias=False)
+        self.lm_head.weight = self.embed.weight                 # tied: the planner keeps it out of FP8
+        for m in self.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                nn.init.normal_(m.weight, std=0.02)
+        self._head32 = None
+
+    def new_cache(self, B, max_len):
+        c, p = self.c, self.embed.weight
+        hd = c["dim"] // c["n_heads"]
+        return [(torch.empty(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device),
+                 torch.empty(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device)) for _ in self.layers]
+
+    def _rope(self, start, T, device):
+        hd = self.c["dim"] // self.c["n_heads"]
+        inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=device, dtype=torch.float32) * 2.0 / hd))
+        ang = torch.arange(start, start + T, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+        return ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
+
+    def forward(self, ids, cache, start=0):
+        """Logits (fp32) for every position of ids [B, T], appending to cache at `start`."""
+        cos, sin = self._rope(start, ids.shape[1], ids.device)
+        x = self.embed(ids)
+        for layer, kv in zip(self.layers, cache):
+            x = layer(x, cos, sin, kv, start)
+        if self._head32 is None or self._head32.device != x.device:
+            self._head32 = self.embed.weight.detach().float()
+        return F.linear(self.norm(x).float(), self._head32)
+
+
+def build(size="c5", dtype=torch.bfloat16, device="cuda", seed=0):
+    torch.manual_seed(seed)
+    return Llama(dict(SIZES[size])).to(device=device, dtype=dtype)
+
+
+@torch.no_grad()
+def generate(model, prompt, n_new):
+    """Greedy decode: prefill the prompt, then n_new single-token steps on the KV cache.
+    Returns (tokens [B, n_new], prefill logits [B, T, V], step logits [B, n_new, V])."""
+    B, T = prompt.shape
+    cache = model.new_cache(B, T + n_new)
+    logits = model(prompt, cache, 0)
+    nxt = logits[:, -1].argmax(-1, keepdim=True)
+    toks, steps = [nxt], [logits[:, -1]]
+    for i in range(1, n_new):
+        lg = model(nxt, cache, T + i - 1)[:, -1]
+        nxt = lg.argmax(-1, keepdim=True)
+        toks.append(nxt)
+        steps.append(lg)
+    return torch.cat(toks, 1), logits, torch.stack(steps, 1)
+
+
+def agreement(ref, got):
+    """cosine (mean over positions), relative L2 and top-1 agreement of two logit tensors."""
+    r, g = ref.reshape(-1, ref.shape[-1]).float(), got.reshape(-1, got.shape[-1]).float()
+    cos = F.cosine_similarity(r, g, dim=-1).mean().item()
+    rel = ((g - r).norm() / r.norm()).item()
+    top1 = (r.argmax(-1) == g.argmax(-1)).float().mean().item()
+    return cos, rel, top1
+
+
+def _median_ms(fn, n):
+    ts = []
+    for _ in range(n):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t) * 1e3)
+    return statistics.median(ts)
+
+
+@torch.no_grad()
+def timings(model, B, prompt_len, n_decode, vocab):
+    ids = torch.randint(0, vocab, (B, prompt_len), device="cuda")
+    cache = model.new_cache(B, prompt_len + n_decode + 8)
+    for _ in range(2):
+        model(ids, cache, 0)
+    prefill = _median_ms(lambda: model(ids, cache, 0), 5)
+    tok = ids[:, -1:]
+    model(tok, cache, prompt_len)
+
+    def steps():
+        for i in range(n_decode):
+            model(tok, cache, prompt_len + i)
+    per_tok = _median_ms(steps, 3) / n_decode
+    return prefill, per_tok
+
+
+def run(size="c5", prompt_len=512, n_decode=128, batches=(1, 8)):
+    from tfp8 import FP8Config, prepare_model
+    from tfp8.linear import FP8Linear
+    from tfp8.planner import weight_bytes
+
+    c = SIZES[size]
+    model = build(size)
+    ids = torch.randint(0, c["vocab"], (1, prompt_len), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+    with torch.no_grad():
+        ref = model(ids, model.new_cache(1, prompt_len), 0)
+    base_t = {B: timings(model, B, prompt_len, n_decode, c["vocab"]) for B in batches}
+    bf16_mb = sum(weight_bytes(model).values()) / 2**20
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn", weight_group=None, nan_check=True))
+    fp8_mb = sum(weight_bytes(model).values()) / 2**20
+    with torch.no_grad():
+        got = model(ids, model.new_cache(1, prompt_len), 0)
+    cos, rel, top1 = agreement(ref, got)
+    print(f"model {size}: {c}")
+    print(f"weights+state bf16 {bf16_mb:.1f} MB -> fp8 {fp8_mb:.1f} MB")
+    print(f"logits vs bf16: cosine {cos:.6f}  relative L2 {rel:.4f}  top-1 {100 * top1:.2f}%")
+    for B in batches:
+        p, d = timings(model, B, prompt_len, n_decode, c["vocab"])
+        pb, db = base_t[B]
+        print(f"B={B}: prefill {prompt_len} tok {p:8.2f} ms (bf16 {pb:8.2f})  decode/token {d:7.3f} ms (bf16 {db:7.3f})  "
+              f"-> {B * prompt_len / p * 1e3:9.0f} prefill tok/s, {B / d * 1e3:8.0f} decode tok/s")
+    paths = {}
+    for m in model.modules():
+        if isinstance(m, FP8Linear):
+            for k, v in m.stats.items():
+                paths[k] = paths.get(k, 0) + v
+    print(f"FP8Linear paths: {paths}")
+    return dict(cos=cos, rel=rel, top1=top1)
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--size", default="c5", choices=list(SIZES))
+    ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--decode", type=int, default=128)
+    a = ap.parse_args()
+    run(a.size, a.prompt_len, a.decode)

@@ -26,3 +26,23 @@ def cpu_forward(x, q, s, group_size, fmt, bias, out_dtype, table=None):
     sv = torch.from_numpy(O.ue8m0_decode(s.numpy())) if s.dtype == torch.uint8 else s.float()
     W = (table[q.long()].float().reshape(N, K // group_size, group_size) * sv[..., None]).reshape(N, K)
     return F.linear(x.float(), W, bias).to(out_dtype)
+
+
+def dequant_weight_f32(q, s, group_size, fmt):
+    """lut[q].float() * scale[n, k//G] on q's own device (tfp8/quantize.py:39-44), so the reference
+    forward can run as an fp32 GPU matmul for model-sized checks.  UE8M0 bytes widen as the
+    oracle does (255 -> NaN, b -> 2^(b-127), exact through ldexp)."""
+    table = lut16(fmt).to(q.device)
+    if s.dtype == torch.uint8:
+        e = s.to(torch.int32)
+        sv = torch.ldexp(torch.ones(e.shape, dtype=torch.float32, device=e.device), e - 127)
+        sv = torch.where(e == 255, torch.full_like(sv, float("nan")), sv)
+    else:
+        sv = s.float()
+    N, K = q.shape
+    return (table[q.long()].float().reshape(N, K // group_size, group_size) * sv[..., None]).reshape(N, K)
+
+
+def ref_linear(x, W, bias, out_dtype):
+    """The reference CPU forward's arithmetic (tfp8/linear.py:179-181) on a pre-dequantized weight."""
+    return F.linear(x.float(), W, bias).to(out_dtype)

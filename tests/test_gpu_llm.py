@@ -1,0 +1,141 @@
+"""C5 end to end: the Llama-style decoder (8 layers, d=2048, 16 heads, SwiGLU 5632, vocab 32000,
+random N(0, 0.02) init) converted by prepare_model to E4M3FN per-channel FP8Linear, prefilled with
+512 tokens and greedily decoded for 128 at batch 1 and batch 8.
+
+Parity: the same model with every FP8Linear replaced by the reference's CPU forward arithmetic
+(tfp8/linear.py:179-181: fp32 F.linear of the dequantized weight, evaluated as an fp32 GPU matmul)
+is run teacher-forced over prompt + generated tokens, and every prefill and decode-step logit row
+is compared.  Both models round each projection to bf16, so they differ by bf16 rounding flips
+that propagate through 8 layers.  The bound is calibrated on that noise: a second reference that
+only changes the fp32 summation order (each projection summed over two K halves) sets the floor,
+and the FP8 model must stay within twice the floor's relative L2 and cosine distance, and within
+3 points of its top-1 agreement (plus absolute bounds: cosine >= 0.999, top-1 >= 90 %).
+One projection is also checked on its live inputs against the float64 oracle with the per-linear
+tolerance of the other GPU tests.  Quality versus the bf16 model (the reference demo's metric,
+demo_llm.py:176-185) is reported.
+"""
+import contextlib
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import cpu_path
+from oracle import fp8_oracle as O
+from tfp8 import FP8Config, prepare_model
+from tfp8.examples import demo_llm
+from tfp8.linear import FP8Linear
+
+pytestmark = pytest.mark.gpu
+
+COS_ABS, TOP1_ABS = 0.999, 0.90
+
+
+class RefLinear(nn.Module):
+    """The reference CPU forward of one FP8Linear, with its weight dequantized once."""
+
+    def __init__(self, f):
+        super().__init__()
+        self.W = cpu_path.dequant_weight_f32(f.qweight, f.weight_scale, f.group_size, f.fmt)
+        self.b = f.bias_f32
+        self.out_dtype = f.out_dtype
+
+    def forward(self, x):
+        return cpu_path.ref_linear(x, self.W, self.b, self.out_dtype)
+
+
+class RefLinearSplitK(RefLinear):
+    """The same arithmetic with another fp32 summation order: two K halves added at the end."""
+
+    def __init__(self, f):
+        super().__init__(f)
+        h = self.W.shape[1] // 2
+        self.lo, self.hi = self.W[:, :h].t().contiguous(), self.W[:, h:].t().contiguous()
+
+    def forward(self, x):
+        h = self.lo.shape[0]
+        xf = x.float()
+        y = (xf[..., :h] @ self.lo) + (xf[..., h:] @ self.hi)
+        if self.b is not None:
+            y = y + self.b
+        return y.to(self.out_dtype)
+
+
+@contextlib.contextmanager
+def swapped(model, table):
+    old = {}
+    for name, new in table.items():
+        parent_name, leaf = name.rsplit(".", 1)
+        parent = model.get_submodule(parent_name)
+        old[name] = getattr(parent, leaf)
+        setattr(parent, leaf, new)
+    try:
+        yield
+    finally:
+        for name, mod in old.items():
+            parent_name, leaf = name.rsplit(".", 1)
+            setattr(model.get_submodule(parent_name), leaf, mod)
+
+
+def test_c5_prefill_and_greedy_decode():
+    T, NEW = 512, 128
+    model = demo_llm.build("c5")
+    c = model.c
+    g = torch.Generator("cuda").manual_seed(7)
+    prompts = {B: torch.randint(0, c["vocab"], (B, T), device="cuda", generator=g) for B in (1, 8)}
+    with torch.no_grad():
+        base = model(prompts[1], model.new_cache(1, T), 0)
+
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn"))
+    fp8 = {n: m for n, m in model.named_modules() if isinstance(m, FP8Linear)}
+    assert len(fp8) == 7 * c["n_layers"]
+    reasons = {d.name: d.reason for d in model._tfp8_plan}
+    assert reasons["lm_head"] == "weight shared with another module (tied)"
+    ref = {n: RefLinear(m) for n, m in fp8.items()}
+    ref2 = {n: RefLinearSplitK(m) for n, m in fp8.items()}
+
+    # live inputs of one projection, for the per-linear oracle check
+    probe_name = "layers.5.mlp.down_proj"
+    seen = []
+    hook = fp8[probe_name].register_forward_hook(lambda m, i, o: seen.append((i[0].detach(), o.detach())))
+    for B in (1, 8):
+        print(f"[c5] B={B}: prefill {T} + greedy {NEW}", flush=True)
+        toks, pre, steps = demo_llm.generate(model, prompts[B], NEW)
+        full = torch.cat([prompts[B], toks[:, :-1]], 1)
+        with torch.no_grad():
+            with swapped(model, ref):
+                rl = model(full, model.new_cache(B, full.shape[1]), 0)
+            with swapped(model, ref2):
+                rl2 = model(full, model.new_cache(B, full.shape[1]), 0)
+        for label, sl in (("prefill", slice(0, T)), ("decode", slice(T - 1, None))):
+            got = pre if label == "prefill" else steps
+            fc, fr, ft = demo_llm.agreement(rl[:, sl], got)
+            nc, nr, nt = demo_llm.agreement(rl[:, sl], rl2[:, sl])
+            print(f"[c5] B={B} {label}: fp8 vs ref cosine {fc:.7f} rel L2 {fr:.2e} top-1 {100 * ft:.2f}% | "
+                  f"noise floor cosine {nc:.7f} rel L2 {nr:.2e} top-1 {100 * nt:.2f}%", flush=True)
+            assert fr <= 2 * nr + 1e-4, (B, label, fr, nr)
+            assert 1 - fc <= 2 * (1 - nc) + 1e-6, (B, label, fc, nc)
+            assert ft >= nt - 0.03 and ft >= TOP1_ABS and fc >= COS_ABS, (B, label, ft, nt, fc)
+        if B == 1:
+            cos, rel, top1 = demo_llm.agreement(base, pre)
+            print(f"[c5] quality vs bf16 model (prefill, B=1): cosine {cos:.5f} rel L2 {rel:.3e} "
+                  f"top-1 {100 * top1:.1f}%", flush=True)
+            assert cos > 0.95   # quantization itself, reported as in the reference demo (no gate there)
+    hook.remove()
+
+    # the probe saw the B=1 prefill (M=512, GEMM), a B=1 decode step (M=1, GEMV), and the B=8 ones
+    f = fp8[probe_name]
+    q, s = f.qweight.cpu().numpy(), f.weight_scale.cpu().numpy()
+    for x, y in (seen[0], seen[1], seen[NEW], seen[NEW + 1]):
+        x2 = x.reshape(-1, x.shape[-1])[:64].float().cpu().numpy().astype(np.float64)
+        y2 = y.reshape(-1, y.shape[-1])[:64].double().cpu().numpy()
+        want = O.linear_ref64(x2, q, s, f.group_size, f.fmt)
+        assert (np.abs(y2 - want) <= O.tolerance(want, "bfloat16")).all(), x.shape
+
+    stats = {}
+    for m in fp8.values():
+        for k, v in m.stats.items():
+            stats[k] = stats.get(k, 0) + v
+    print(f"[c5] FP8Linear paths {stats}", flush=True)
+    assert stats["gemv"] > 0 and stats["gemm"] + stats["chunked"] > 0 and stats["fallback"] == 0

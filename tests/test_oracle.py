@@ -269,3 +269,15 @@ def test_cpu_path_matches_oracle():
         y = cpu_path.cpu_forward(torch.from_numpy(x), torch.from_numpy(q), torch.from_numpy(s), GG, fmt, None,
                                  torch.float32)
         assert (np.abs(y.double().numpy() - ref) <= O.tolerance(ref, "float32")).all()
+
+
+def test_cpu_path_dequant_weight_f32_matches_oracle():
+    rng = np.random.default_rng(12)
+    q = rng.integers(0, 256, (24, 128)).astype(np.uint8)
+    for fmt in FMTS:
+        for s in (rng.random((24, 4)).astype(np.float32) + 0.25,
+                  np.concatenate([rng.integers(0, 256, (23, 4)), [[0, 1, 254, 255]]]).astype(np.uint8)):
+            want = O.dequantize_weight(q, s, fmt, 32)
+            got = cpu_path.dequant_weight_f32(torch.from_numpy(q), torch.from_numpy(s), 32, fmt).numpy()
+            same = (got == want) | (np.isnan(got) & np.isnan(want))
+            assert same.all(), fmt
