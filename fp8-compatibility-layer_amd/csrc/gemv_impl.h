@@ -15,9 +15,9 @@
 //     group's resource -- the hardware returns zeros for all of them, so the main loop has no
 //     branches around memory and the compiler can wait for exactly the load it needs;
 //   * the activation rows (M x K, native dtype) and the K-group scales of the block's rows (as
-//     f32) are copied once per block into LDS; finished rows are reduced into LDS and each wave
-//     writes its own rows out (with per-channel scale and bias) after its loop, so the loop issues
-//     no global stores either;
+//     f32) are copied once per block into LDS; when a row group is finished the wave reduces it
+//     and writes its R adjacent outputs per activation row (with per-channel scale and bias) in
+//     one packed store -- at the end of a GEMV the output stores are on the critical path;
 //   * codes are decoded in registers with v_cvt_scalef32_pk_{bf16,f16}_{fp8,bf8} (2 codes per
 //     instruction), no LDS table; 16-bit activations are multiplied with v_dot2_f32_{bf16,f16}
 //     (exact products, fp32 accumulation); fp32 activations use v_cvt_pk_f32_fp8 and fp32 FMA;
@@ -63,6 +63,30 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX));
 }
 
+// R consecutive outputs y[o .. o+R) of runtime dtype: one 2R- or 4R-byte store when `pack`
+// (o % R == 0 and y aligned), else one element at a time; only the first nval are written.
+template <int R>
+__device__ __forceinline__ void store_rows(void* y, size_t o, int ydt, const float (&v)[R], int nval, bool pack) {
+    if (pack && nval == R) {
+        if (ydt == TFP8_F32) {
+            if constexpr (R == 2) { *(float2*)((float*)y + o) = make_float2(v[0], v[1]); return; }
+            if constexpr (R == 4) { *(float4*)((float*)y + o) = make_float4(v[0], v[1], v[2], v[3]); return; }
+        } else {
+            uint32_t h[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) h[r] = ydt == TFP8_BF16 ? f32_to_bf16_bits(v[r]) : f32_to_f16_bits(v[r]);
+            if constexpr (R == 2) { *(uint32_t*)((uint16_t*)y + o) = h[0] | (h[1] << 16); return; }
+            if constexpr (R == 4) {
+                *(uint2*)((uint16_t*)y + o) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                return;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nval) store_elem(y, o + r, ydt, v[r]);
+}
+
 template <int MT, int XDT, int FMT, bool GROUPED, int R, int U, int TPB, bool XLDS>
 __global__ __launch_bounds__(TPB) void gemv_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ w, const void* __restrict__ ws, int sk,
@@ -75,7 +99,12 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     // The wave index is wave-uniform; readfirstlane makes every cursor and row base below scalar.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ngr = (N + R - 1) / R;                         // row groups
-    const int gb = blockIdx.x * per_block;                   // first row group of this block
+    // Blocks are dispatched round-robin over the 8 XCDs; renumber them so that each XCD owns one
+    // contiguous run of rows (a bijection for any grid size).  Each 128-byte line of y is then
+    // written from a single XCD's L2 instead of partially from all eight.
+    const int nblk = gridDim.x, xcd = blockIdx.x & 7, q8 = nblk >> 3, r8 = nblk & 7;
+    const int lb = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const int gb = lb * per_block;                           // first row group of this block
     const int ge = min(ngr, gb + per_block);
     const int nmine = ge - gb > wave ? (ge - gb - wave + GEMV_WAVES - 1) / GEMV_WAVES : 0;
     const int cpr = (K + GEMV_CHUNK - 1) / GEMV_CHUNK;       // chunks per row
@@ -83,7 +112,6 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     const int row0 = gb * R;                                 // first row of this block
     const int rows_b = min(N, ge * R) - row0;                // rows of this block
     float* ssc = (float*)(smem + xlds_bytes);                // block scales, f32 [rows][ng] or [rows]
-    float* sout = (float*)(smem + xlds_bytes + slds_bytes);  // block results [rows][MT]
 
     const uint32_t lane16 = (uint32_t)lane * 16u;
     // Vector offset of the last chunk of a row: lanes past K read out of range (zeros).
@@ -121,7 +149,9 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     // cover a weight load.
     const int srows = max(rows_b, 0);
     const int scount = GROUPED ? srows * ng : srows;         // f32 scale values staged
-    float* sbias = sout + per_block * R * MT;                // [rows]
+    float* sbias = (float*)(smem + xlds_bytes + slds_bytes); // [rows]
+    // R adjacent outputs go out as one store when y and every row's offset allow it.
+    const bool ypack = R > 1 && (reinterpret_cast<uintptr_t>(y) % (R * (ydt == TFP8_F32 ? 4 : 2))) == 0 && ldy % R == 0;
     const bool ue8 = sk == TFP8_SCALE_UE8M0;
     const size_t s0 = GROUPED ? (size_t)row0 * ng : (size_t)row0;
     const __amdgpu_buffer_rsrc_t srs = buf_rsrc(ws, (uint32_t)((size_t)N * ng * (ue8 ? 1 : 4)));
@@ -254,17 +284,28 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
                         }
                     }
                 if (last) {
-                    // Row group finished: wave sums into LDS (lane m holds row m's value).
+                    // Row group finished: lane m takes the R row totals of activation row m and
+                    // writes them straight to y, R adjacent outputs in one store when aligned.
+                    float v[R];
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        float v = 0.f;
+                        float t = 0.f;
 #pragma unroll
                         for (int m = 0; m < MT; ++m) {
                             const float tot = wave_sum(acc[r][m]);
-                            v = lane == m ? tot : v;
+                            t = lane == m ? tot : t;
                             acc[r][m] = 0.f;
                         }
-                        if (rl + r < rows_b && lane < MT) sout[(rl + r) * MT + lane] = v;
+                        v[r] = t;
+                    }
+                    if (lane < M) {
+                        const int nval = min(R, rows_b - rl);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const int rr = min(rl + r, rows_b - 1);
+                            v[r] = v[r] * (GROUPED ? 1.f : ssc[rr]) + sbias[rr];
+                        }
+                        store_rows<R>(y, (size_t)lane * ldy + row0 + rl, ydt, v, nval, ypack);
                     }
                 }
                 if (++cc == cpr) { cc = 0; ++ct; }
@@ -281,24 +322,15 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
         if (i0 + 3 * U < items) issue(sb);
     }
 
-    // ---------------------------------------------------------------- epilogue: this wave's rows
-    // Each wave wrote only its own rows' sums into LDS, so it stores them without a block barrier.
-    for (int i = lane; i < nmine * R * MT; i += 64) {
-        const int t = i / (R * MT), rm = i - t * (R * MT), r = rm / MT, m = rm - r * MT;
-        const int rl = (wave + GEMV_WAVES * t) * R + r;
-        if (m >= M || rl >= rows_b) continue;
-        const int n = row0 + rl;
-        float v = sout[rl * MT + m];
-        if constexpr (!GROUPED) v *= ssc[rl];
-        store_elem(y, (size_t)m * ldy + n, ydt, v + sbias[rl]);
-    }
 }
 
 // Compiled configurations (id, R, U, waves per CU, threads per block); gemv_pick() chooses one
 // by shape and TFP8_GEMV_CFG=<id> overrides it.
 #ifdef TFP8_GEMV_SWEEP
 #define TFP8_GEMV_CFG_LIST X(0, 1, 2, 32, 256) X(1, 1, 2, 64, 256) X(2, 1, 2, 64, 512) X(3, 1, 2, 64, 1024) \
-    X(4, 2, 2, 32, 256) X(5, 2, 2, 32, 1024) X(6, 1, 4, 32, 1024) X(7, 4, 2, 16, 256) X(8, 2, 4, 16, 512)
+    X(4, 2, 2, 32, 256) X(5, 2, 2, 32, 1024) X(6, 1, 4, 32, 1024) X(7, 4, 2, 16, 256) X(8, 2, 4, 16, 512) \
+    X(9, 2, 1, 32, 256) X(10, 2, 4, 32, 256) X(11, 2, 2, 32, 512) X(12, 1, 4, 32, 256) X(13, 4, 1, 32, 256) \
+    X(14, 1, 1, 32, 256) X(15, 2, 2, 32, 128) X(16, 1, 2, 32, 128)
 #else
 #define TFP8_GEMV_CFG_LIST X(2, 1, 2, 64, 512) X(4, 2, 2, 32, 256) X(8, 2, 4, 16, 512)
 #endif
@@ -353,7 +385,7 @@ static void launch_rows(int waves_per_cu, const void* x, const uint8_t* w, const
     grid = (ngr + per_block - 1) / per_block;
     const size_t xbytes = (size_t)M * K * (XDT == TFP8_F32 ? 4 : 2);
     const size_t sbytes = ((size_t)per_block * R * (GROUPED ? ng : 1) * 4 + 15) / 16 * 16;
-    const size_t obytes = (size_t)per_block * R * (MT + 1) * 4;   // results + bias
+    const size_t obytes = (size_t)per_block * R * 4;   // bias
     bool xlds = xbytes + sbytes + obytes <= (size_t)di.lds;
 #ifdef TFP8_GEMV_SWEEP
     if (gemv_env_int("TFP8_GEMV_XG", 0)) xlds = false;
