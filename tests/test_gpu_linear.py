@@ -302,3 +302,33 @@ def test_tiled_gemm_every_config(tile, monkeypatch):
         _run(40, 200, 1120, None, torch.float16, xdt=torch.float16, seed=tile)
         _run(130, 72, 640, 32, torch.bfloat16, xdt=torch.bfloat16, seed=tile + 1)
         _run(257, 136, 704, 64, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", seed=tile + 2)
+
+
+def test_split_k_workspace_contents_do_not_matter(monkeypatch):
+    """Split-K through the caller's workspace (fp32 partial tiles, then the reduce kernel): a
+    workspace full of garbage, or one reused from the previous call, gives the same bits every
+    time, within the oracle tolerance."""
+    monkeypatch.setenv("TFP8_GEMM_V1", "1")
+    monkeypatch.setenv("TFP8_GEMM_TILE", "13")
+    monkeypatch.setenv("TFP8_GEMM_SPLITK", "3")
+    lib = _ext.require()
+    M, N, K = 200, 512, 3072
+    q, s, G, b = _layer(N, K, None, "e4m3fn", "ue8m0", seed=21)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(22)).half().cuda()
+    nb = lib.tfp8_linear_workspace_size(_ext.DTYPE_ID[x.dtype], M, N, K)
+    assert nb > 0
+    ws = torch.full((nb,), 0xFF, dtype=torch.uint8, device="cuda")
+    outs = []
+    for rep in range(3):
+        if rep == 2:
+            ws.random_(0, 256)
+        y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        rc = lib.tfp8_linear(x.data_ptr(), _ext.DTYPE_ID[x.dtype], M, K, q.data_ptr(), N, s.data_ptr(),
+                             _ext.scale_kind(s), G, _ext.FMT_ID["e4m3fn"], b.data_ptr(), y.data_ptr(),
+                             _ext.DTYPE_ID[torch.float16], ws.data_ptr(), nb,
+                             torch._C._cuda_getCurrentRawStream(0))
+        assert rc == 0, _ext.last_error()
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    _check(outs[0], x, q, s, G, "e4m3fn", b, torch.float16, "gemm", "split-K arrival")
