@@ -480,6 +480,9 @@ void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws
 int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
                     const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
                     float* partial, hipStream_t s);
+int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, const uint8_t* w, int N, const void* ws,
+                  int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
+int gemv_mfma_min_m();
 
 template <typename T, int FMT, int BM, int BN, int WM, int WN, int BK>
 static void launch_gemm_cfg(const void* x, const float* xs, const uint8_t* w, const void* ws, int sk,
@@ -528,7 +531,12 @@ static int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } retu
 int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
              const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, float* partial,
              hipStream_t s) {
-    // The weight-streaming kernel takes most shapes; the LDS-tiled kernel below is the general path.
+    // Decode sizes go to the matrix-core decode kernel (no split-K), then the weight-streaming
+    // kernel (which is as fast from 9 rows up); the LDS-tiled kernel below is the general path.
+    if (M <= 8 && M >= gemv_mfma_min_m()) {
+        const int rm = run_gemv_mfma(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
+        if (rm != 1) return rm;
+    }
     const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
     if (rs != 1) return rs;
     const int ng = K / G;

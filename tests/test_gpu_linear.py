@@ -332,3 +332,19 @@ def test_split_k_workspace_contents_do_not_matter(monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     _check(outs[0], x, q, s, G, "e4m3fn", b, torch.float16, "gemm", "split-K arrival")
+
+
+@pytest.mark.parametrize("nt,w,d", [(2, 8, 4), (2, 8, 8), (2, 4, 4), (2, 4, 8), (1, 8, 4), (1, 8, 8), (1, 4, 4), (1, 4, 8)])
+def test_decode_mfma_every_config(nt, w, d, monkeypatch):
+    """The matrix-core decode kernel (M <= 8 rows) in every compiled configuration, forced down to
+    M = 1: rows past N in the last block, a K tail that is not a whole 64-byte chunk, K ranges that
+    leave some waves without work, per-channel / f32 K-group (G=64) / UE8M0 K-group (G=32) scales,
+    both formats, f16 and bf16 activations, with and without bias."""
+    monkeypatch.setenv("TFP8_GEMV_MFMA_MIN", "1")
+    monkeypatch.setenv("TFP8_GM_NT", str(nt))
+    monkeypatch.setenv("TFP8_GM_W", str(w))
+    monkeypatch.setenv("TFP8_GM_D", str(d))
+    _run(1, 72, 720, None, torch.bfloat16, xdt=torch.bfloat16, seed=nt * 100 + w * 10 + d)   # K tail 16
+    _run(5, 200, 1152, 64, torch.float16, xdt=torch.float16, seed=nt + w + d)
+    _run(8, 136, 544, 32, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", bias=False, seed=d)  # tail 32
+    _run(3, 40, 96, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=w)
