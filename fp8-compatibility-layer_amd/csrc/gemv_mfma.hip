@@ -218,6 +218,7 @@ static void gm_pick(int NT, int W, int D, const void* x, const float* xs, const 
     }
     TFP8_GM_CFG(2, 8, 4) TFP8_GM_CFG(2, 8, 8) TFP8_GM_CFG(2, 4, 4) TFP8_GM_CFG(2, 4, 8)
     TFP8_GM_CFG(1, 8, 4) TFP8_GM_CFG(1, 8, 8) TFP8_GM_CFG(1, 4, 4) TFP8_GM_CFG(1, 4, 8)
+    TFP8_GM_CFG(4, 4, 4) TFP8_GM_CFG(4, 8, 4) TFP8_GM_CFG(4, 4, 2) TFP8_GM_CFG(2, 4, 2)
 #undef TFP8_GM_CFG
     gm_launch<T, FMT, SMODE, 2, 8, 4>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, s);
 }
