@@ -245,3 +245,45 @@ def test_available_false_and_require_raises_without_gpu():
     assert _ext.available() is False
     with pytest.raises(RuntimeError):
         _ext.require()
+
+
+@pytest.mark.parametrize("group,sf", [(None, "f32"), (32, "ue8m0")])
+def test_fp8_checkpoint_roundtrip(tmp_path, group, sf):
+    """save_fp8 / load_fp8: a converted model written with float8 code tensors and its scales is
+    rebuilt from an unconverted model of the same architecture, with identical outputs; tied
+    weights are stored once."""
+    from safetensors import safe_open
+
+    from tfp8 import FP8Config, load_fp8, prepare_model, save_fp8
+    from tfp8.examples import demo_llm
+
+    cfg = dict(dim=1024, n_layers=1, n_heads=8, n_kv=8, ffn=1024, vocab=64)
+    torch.manual_seed(0)
+    model = demo_llm.Llama(cfg)
+    prepare_model(model, "llm", FP8Config(weight_group=group, scale_format=sf, nan_check=False))
+    ids = torch.randint(0, 64, (1, 8))
+    with torch.no_grad():
+        want = model(ids, model.new_cache(1, 8), 0)
+    path = str(tmp_path / "m.safetensors")
+    save_fp8(model, path, metadata={"note": "test"})
+
+    with safe_open(path, framework="pt") as f:
+        keys = set(f.keys())
+        meta = f.metadata()
+        q = f.get_tensor("layers.0.mlp.up_proj.qweight")
+        s = f.get_tensor("layers.0.mlp.up_proj.weight_scale")
+    assert q.dtype == torch.float8_e4m3fn and q.shape == (1024, 1024)
+    assert s.dtype == (torch.uint8 if sf == "ue8m0" else torch.float32)
+    assert s.shape == (1024, 1024 // (group or 1024))
+    assert "lm_head.weight" not in keys and meta["tfp8.alias.lm_head.weight"] == "embed.weight"
+    assert meta["note"] == "test" and meta["tfp8.format"] == "1"
+    assert sum(k.startswith("tfp8.layer.") for k in meta) == 7
+
+    torch.manual_seed(1)
+    fresh = demo_llm.Llama(cfg)
+    load_fp8(fresh, path, nan_check=False)
+    assert sum(isinstance(m, FP8Linear) for m in fresh.modules()) == 7
+    assert fresh.lm_head.weight.data_ptr() == fresh.embed.weight.data_ptr()
+    with torch.no_grad():
+        got = fresh(ids, fresh.new_cache(1, 8), 0)
+    assert torch.equal(want, got)
