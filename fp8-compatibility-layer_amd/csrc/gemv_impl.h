@@ -171,7 +171,8 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
         for (int q = 0; q < XC; ++q) xcp[q] = buf_load16(xr, (uint32_t)(tid + q * GEMV_THREADS) * 16u, 0);
     }
     const uint32_t scp = tid < scount ? scale_raw(tid) : 0u;
-    const uint32_t bcp = __builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + tid) * 4, 0, 0);
+    // (no bias: no load -- every load instruction here costs address-unit time the weights need)
+    const uint32_t bcp = bias ? __builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + tid) * 4, 0, 0) : 0u;
 
     issue(sa);
     issue(sb);
@@ -185,8 +186,11 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
     if (tid < scount) ssc[tid] = scale_f32(scp);
     for (int i = tid + GEMV_THREADS; i < scount; i += GEMV_THREADS) ssc[i] = scale_f32(scale_raw(i));
     if (tid < srows) sbias[tid] = __uint_as_float(bcp);
-    for (int i = tid + GEMV_THREADS; i < srows; i += GEMV_THREADS)
-        sbias[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + i) * 4, 0, 0));
+    if (bias)
+        for (int i = tid + GEMV_THREADS; i < srows; i += GEMV_THREADS)
+            sbias[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs, (row0 + i) * 4, 0, 0));
+    else
+        for (int i = tid + GEMV_THREADS; i < srows; i += GEMV_THREADS) sbias[i] = 0.f;
     __syncthreads();
 
     // ---------------------------------------------------------------- compute side
@@ -330,9 +334,9 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
 #define TFP8_GEMV_CFG_LIST X(0, 1, 2, 32, 256) X(1, 1, 2, 64, 256) X(2, 1, 2, 64, 512) X(3, 1, 2, 64, 1024) \
     X(4, 2, 2, 32, 256) X(5, 2, 2, 32, 1024) X(6, 1, 4, 32, 1024) X(7, 4, 2, 16, 256) X(8, 2, 4, 16, 512) \
     X(9, 2, 1, 32, 256) X(10, 2, 4, 32, 256) X(11, 2, 2, 32, 512) X(12, 1, 4, 32, 256) X(13, 4, 1, 32, 256) \
-    X(14, 1, 1, 32, 256) X(15, 2, 2, 32, 128) X(16, 1, 2, 32, 128)
+    X(14, 1, 1, 32, 256) X(15, 2, 2, 32, 128) X(16, 1, 2, 32, 128) X(17, 2, 2, 28, 448) X(18, 1, 2, 56, 448)
 #else
-#define TFP8_GEMV_CFG_LIST X(2, 1, 2, 64, 512) X(4, 2, 2, 32, 256) X(8, 2, 4, 16, 512)
+#define TFP8_GEMV_CFG_LIST X(2, 1, 2, 64, 512) X(4, 2, 2, 32, 256) X(8, 2, 4, 16, 512) X(17, 2, 2, 28, 448)
 #endif
 
 static inline int gemv_env_int(const char* name, int dflt) {
