@@ -1,0 +1,564 @@
+// W8A8: FP8 activations x FP8 weights with 32-wide K-block scales (reference fp8_cuda.py and
+// fp8_gemm_kernel.cu), on gfx950 matrix cores.
+//
+//   quantize:  per row and 32-wide K block, s = max(amax / max_finite, 1e-12); with UE8M0,
+//              e = clamp(ceil(log2 s), -127, 127), s = 2^e and the stored byte is e + 127;
+//              q = encode(clamp(x / s, +-max_finite))                      (fp8_cuda.py:74-92)
+//   GEMM:      C[m,n] = sum_kb sa[m,kb] * sb[n,kb] * sum_{k in kb} A[m,k] * B[k,n] + bias[n]
+//              (block mode), or (sum_k A B) * sa[m] * sb[n] + bias[n] (row/col mode)
+//                                                                      (fp8_gemm_kernel.cu:41-118)
+//
+// The weight operand is taken transposed, Bt[N,K] (k contiguous, as the quantizer writes it):
+// both MFMA operands then load as contiguous k runs.  One v_mfma_f32_16x16x32_{fp8,bf8}_{fp8,bf8}
+// covers one 32-wide block of a 16 x 16 output tile exactly; its fp32 result is multiplied by the
+// row x column scale product and accumulated in fp32 (products of two FP8 values are exact in
+// fp32).  Tiles: 64 x 64 per block of 4 waves (2 x 2, each 32 x 32 = 2 x 2 MFMA tiles), 128-wide
+// K steps staged through registers into a double-buffered LDS pair with the scales of the step.
+#include "tfp8_common.h"
+
+namespace tfp8 {
+
+namespace {
+
+constexpr int W8_BM = 64, W8_BN = 64, W8_BK = 128, W8_KB = W8_BK / 32;
+constexpr int W8_ROW = W8_BK + 16;   // LDS row stride (bytes): 16-byte pad
+constexpr uint32_t W8_FLAGS = 0x00020000u;
+constexpr uint32_t W8_OOB = 0x80000000u;
+enum { W8_BLOCK = 0, W8_ROWCOL = 1 };
+
+template <int FA, int FB>
+__device__ __forceinline__ f32x4 w8_mma(long a, long b, f32x4 c) {
+    if constexpr (FA == TFP8_E4M3FN && FB == TFP8_E4M3FN) return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, b, c, 0, 0, 0);
+    else if constexpr (FA == TFP8_E4M3FN) return __builtin_amdgcn_mfma_f32_16x16x32_fp8_bf8(a, b, c, 0, 0, 0);
+    else if constexpr (FB == TFP8_E4M3FN) return __builtin_amdgcn_mfma_f32_16x16x32_bf8_fp8(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_bf8_bf8(a, b, c, 0, 0, 0);
+}
+
+template <bool UE8M0>
+__device__ __forceinline__ float w8_scale(const void* p, size_t i) {
+    if constexpr (UE8M0) return ue8m0_to_f32(((const uint8_t*)p)[i]);
+    else return ((const float*)p)[i];
+}
+
+// ------------------------------------------------------------------ quantizer
+// One thread per 32-value block (the blocks of a row are consecutive in memory).  A block holding
+// a NaN gets a NaN scale (UE8M0 byte 255, the kernel contract's NaN) and NaN codes 0x7F, as
+// torch's amax and division propagate it; an infinite amax gives scale inf (UE8M0: 2^127).
+template <int FMT, int XDT, bool UE8M0>
+__global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict__ x, int R, int K,
+                                                          uint8_t* __restrict__ q, void* __restrict__ scale) {
+    using F = Fmt<FMT>;
+    const int kb_n = K / 32;
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (int64_t)R * kb_n) return;
+    const size_t base = (size_t)blk * 32;   // row-major [R, K]: block blk starts at element 32*blk
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = load_elem<XDT>(x, base + i);
+    float amax = 0.f;
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));     // fmaxf skips NaN operands: they are tracked apart
+        nan |= v[i] != v[i];
+    }
+    float s = nan ? __builtin_nanf("") : fmaxf(amax / F::MAX_FINITE, 1e-12f);
+    if constexpr (UE8M0) {
+        uint8_t byte = 0xFFu;
+        if (!nan) {
+            int e = 127;
+            if (s != __builtin_inff()) {
+                int ex;
+                const float m = frexpf(s, &ex);  // s = m * 2^ex, m in [0.5, 1): ceil(log2 s) exactly
+                e = max(-127, min(127, m == 0.5f ? ex - 1 : ex));
+            }
+            s = ldexpf(1.f, e);
+            byte = (uint8_t)(e + 127);
+        }
+        ((uint8_t*)scale)[blk] = byte;
+    } else {
+        ((float*)scale)[blk] = s;
+    }
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float d = v[4 * i + j] / s;
+            const uint32_t code = d != d ? 0x7Fu : encode_fp8<FMT>(fminf(fmaxf(d, -F::MAX_FINITE), F::MAX_FINITE));
+            word |= code << (8 * j);
+        }
+        w[i] = word;
+    }
+    uint4* dst = (uint4*)(q + base);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// ------------------------------------------------------------------ GEMM
+// Two kernels share the tiling below and differ in what the matrix cores multiply:
+//
+//   w8_f16_kernel (default): FP8 codes are decoded to f16 once per tile (exact: every FP8 value
+//     is an f16) and multiplied by v_mfma_f32_16x16x32_f16, whose products reach the fp32
+//     accumulator exactly -- the numerics of the reference's fp16 WMMA (fp8_gemm_kernel.cu:72-99).
+//     One MFMA covers exactly one 32-wide scale block of a 16 x 16 tile; in block mode its result
+//     is multiplied by sa * sb and accumulated in fp32 (fp8_gemm_kernel.cu:74-93), in row/column
+//     mode MFMAs accumulate directly and the scales go to the epilogue (:105-113).
+//   w8_mx_kernel (native FP8): the codes go to the FP8 matrix cores as they are.  Those align
+//     the products of one dot product to the largest and keep about 13 fraction bits (measured:
+//     2^16 + 2^0 sums to 2^16), so results differ from an fp32 sum by ~1e-5..1e-4 of max|C|.
+//     UE8M0 block scales ride in v_mfma_scale_f32_16x16x128_f8f6f4 (one E8M0 byte per lane);
+//     row/column scales use the unscaled instruction; FP32 block scales use four
+//     v_mfma_f32_16x16x32 per 128-step with the fp32 multiply-accumulate above.
+//
+// Tiling: block tile BT x BT of C, 4 waves in 2 x 2, each owning (BT/2) x (BT/2) = TI x TI MFMA
+// tiles of 16 x 16; K advances 128 per step.  Each step's A and Bt tiles (BT rows x 128 codes,
+// k contiguous) are loaded into registers one step ahead and written (decoded, for the f16
+// kernel) to the other half of a double-buffered LDS pair, so one barrier per step suffices.
+// Out-of-range rows and the K tail read as zero through buffer-load bounds.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// XCD-aware tile order: consecutive blocks go to the 8 XCDs in turn; renumber so each XCD owns a
+// contiguous run, then walk that run in groups of 8 tile rows so co-resident blocks share A and
+// Bt panels in their XCD's L2.
+__device__ __forceinline__ void w8_tile(int M, int N, int BT, int& m0, int& n0) {
+    const int nbm = (M + BT - 1) / BT, nbn = (N + BT - 1) / BT, nblk = nbm * nbn;
+    const int xcd = blockIdx.x & 7, q8 = nblk >> 3, r8 = nblk & 7;
+    const int lb = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    constexpr int GM = 8;
+    const int grp = lb / (GM * nbn), first = grp * GM, gsz = min(nbm - first, GM), in = lb % (GM * nbn);
+    m0 = (first + in % gsz) * BT;
+    n0 = (in / gsz) * BT;
+}
+
+// Per-step operand loader: BT rows x 128 codes of A (op 0) and Bt (op 1), CH 16-byte chunks per
+// thread and operand, plus (block mode) the step's 4 scales per row as fp32 words.
+template <int BT, bool UE8M0, bool BLOCK_SCALES>
+struct W8Loader {
+    static constexpr int CH = BT * 8 / 256;
+    static constexpr int NSW = BLOCK_SCALES ? 2 * BT * 4 / 256 : 1;
+    static_assert(BT * 4 % 256 == 0, "scale words of one operand must fill whole thread sweeps");
+    __amdgpu_buffer_rsrc_t rs[2], rss[2];
+    int K, nkb;
+    uint4 rt[2][CH];
+    float rsc[NSW];
+
+    __device__ __forceinline__ W8Loader(const uint8_t* a, const void* sa, const uint8_t* bt, const void* sb, int M,
+                                        int N, int K_, int m0, int n0)
+        : K(K_), nkb(K_ / 32) {
+        const uint32_t ra = (uint32_t)min(BT, M - m0), rb = (uint32_t)min(BT, N - n0);
+        rs[0] = __builtin_amdgcn_make_buffer_rsrc((void*)(a + (size_t)m0 * K), (short)0, (int)(ra * (uint32_t)K),
+                                                  (int)W8_FLAGS);
+        rs[1] = __builtin_amdgcn_make_buffer_rsrc((void*)(bt + (size_t)n0 * K), (short)0, (int)(rb * (uint32_t)K),
+                                                  (int)W8_FLAGS);
+        constexpr int SB = UE8M0 ? 1 : 4;
+        rss[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb * SB), (short)0,
+                                                   (int)(ra * (uint32_t)nkb * SB), (int)W8_FLAGS);
+        rss[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb * SB), (short)0,
+                                                   (int)(rb * (uint32_t)nkb * SB), (int)W8_FLAGS);
+    }
+    __device__ __forceinline__ void load(int kt, int tid) {
+#pragma unroll
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int ch = tid + i * 256, row = ch >> 3, col = (ch & 7) * 16;
+                const uint32_t off = kt + col < K ? (uint32_t)row * (uint32_t)K + (uint32_t)(kt + col) : W8_OOB;
+                rt[op][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)off, 0, 0));
+            }
+        if constexpr (BLOCK_SCALES) {
+            const int kb0 = kt / 32;
+#pragma unroll
+            for (int i = 0; i < NSW; ++i) {
+                // BT * 4 is a multiple of 256 and tid < 256: the operand depends on i only
+                const int w = tid + i * 256, op = i * 256 / (BT * 4), row = (w >> 2) % BT, q = w & 3;
+                const bool ok = kb0 + q < nkb;
+                if constexpr (UE8M0) {
+                    const uint32_t o = ok ? (uint32_t)(row * nkb + kb0 + q) : W8_OOB;
+                    rsc[i] = ue8m0_to_f32((uint8_t)__builtin_amdgcn_raw_buffer_load_b8(rss[op], (int)o, 0, 0));
+                } else {
+                    const uint32_t o = ok ? (uint32_t)((row * nkb + kb0 + q) * 4) : W8_OOB;
+                    rsc[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rss[op], (int)o, 0, 0));
+                }
+            }
+        }
+    }
+};
+
+// Epilogue: C[m, n] = acc (+ row/column scales) + bias[n], fp32, row-major.
+template <int TI, int BT, bool UE8M0, int MODE>
+__device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TI], const void* sa, const void* sb, const float* bias,
+                                         float* c, int M, int N, int m0, int n0, int wm, int wn, int lane) {
+    const int frow = lane & 15, orow = 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < TI; ++j) {
+        const int n = n0 + wn * (BT / 2) + j * 16 + frow;
+        if (n >= N) continue;
+        const float bv = bias ? bias[n] : 0.f;
+        const float cs = MODE == W8_ROWCOL ? w8_scale<UE8M0>(sb, (size_t)n) : 1.f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * (BT / 2) + i * 16 + orow + r;
+                if (m >= M) continue;
+                float v = acc[i][j][r];
+                if constexpr (MODE == W8_ROWCOL) v = v * w8_scale<UE8M0>(sa, (size_t)m) * cs;
+                c[(size_t)m * N + n] = v + bv;
+            }
+    }
+}
+
+// ---- exact kernel: f16 tiles in LDS.  A row of a tile is 128 halves = 16 chunks of 8; chunk u
+// (k = 8u .. 8u+7) of row r sits at chunk u ^ (r & 15), so the 16 rows read by one ds_read_b128
+// of a fragment land on 16 distinct 4-bank groups.  Lane l of an MFMA for scale block q reads
+// row l & 15, chunk 4q + (l >> 4): k = 32q + 8 (l >> 4) + 0..7, the instruction's own k order.
+template <int FA, int FB, bool UE8M0, int MODE>
+__global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
+                                                     const uint8_t* __restrict__ bt, const void* __restrict__ sb,
+                                                     const float* __restrict__ bias, float* __restrict__ c, int M,
+                                                     int N, int K) {
+    constexpr int BT = 128, TI = BT / 32;
+    constexpr bool BLK = MODE == W8_BLOCK;
+    using L = W8Loader<BT, UE8M0, BLK>;
+    __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 256];       // [buffer][A, Bt][row * 256 B]
+    __shared__ __attribute__((aligned(16))) float sS[2][2][BLK ? BT * 4 : 1];  // [buffer][A, Bt][row * 4 + q]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int m0, n0;
+    w8_tile(M, N, BT, m0, n0);
+    L ld(a, sa, bt, sb, M, N, K, m0, n0);
+    const int ntile = (K + 127) / 128;
+
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < L::CH; ++i) {
+                const int ch = tid + i * 256, row = ch >> 3, cc = ch & 7, sw = row & 15;
+                const uint4 v = ld.rt[op][i];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+                uint32_t h[8];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    h[2 * d] = op == 0 ? cvt2_f16<FA>(w[d], false) : cvt2_f16<FB>(w[d], false);
+                    h[2 * d + 1] = op == 0 ? cvt2_f16<FA>(w[d], true) : cvt2_f16<FB>(w[d], true);
+                }
+                uint8_t* base = &sT[buf][op][row * 256];
+                *(uint4*)(base + 16 * ((2 * cc) ^ sw)) = make_uint4(h[0], h[1], h[2], h[3]);
+                *(uint4*)(base + 16 * ((2 * cc + 1) ^ sw)) = make_uint4(h[4], h[5], h[6], h[7]);
+            }
+        if constexpr (BLK) {
+#pragma unroll
+            for (int i = 0; i < L::NSW; ++i) {
+                const int w = tid + i * 256;
+                sS[buf][i * 256 / (BT * 4)][w % (BT * 4)] = ld.rsc[i];
+            }
+        }
+    };
+
+    f32x4 acc[TI][TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int frow = lane & 15, g = lane >> 4;
+    auto frag = [&](int buf, int op, int row, int q) -> f16x8 {
+        return *(const f16x8*)&sT[buf][op][row * 256 + 16 * ((4 * q + g) ^ frow)];
+    };
+
+    ld.load(0, tid);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < ntile; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < ntile) ld.load((t + 1) * 128, tid);
+        f16x8 bf[TI][4];
+#pragma unroll
+        for (int j = 0; j < TI; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bf[j][q] = frag(buf, 1, wn * (BT / 2) + j * 16 + frow, q);
+        if constexpr (BLK) {
+            float4 sbv[TI];
+#pragma unroll
+            for (int j = 0; j < TI; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * (BT / 2) + j * 16 + frow) * 4];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                f16x8 af[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) af[q] = frag(buf, 0, wm * (BT / 2) + i * 16 + frow, q);
+                float4 sav[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sav[r] = *(const float4*)&sS[buf][0][(wm * (BT / 2) + i * 16 + 4 * g + r) * 4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {   // blocks past K hold zero codes and finite scales
+#pragma unroll
+                    for (int j = 0; j < TI; ++j) {
+                        const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q], bf[j][q], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        const float sbq = q == 0 ? sbv[j].x : q == 1 ? sbv[j].y : q == 2 ? sbv[j].z : sbv[j].w;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float saq = q == 0 ? sav[r].x : q == 1 ? sav[r].y : q == 2 ? sav[r].z : sav[r].w;
+                            acc[i][j][r] = fmaf(p[r], saq * sbq, acc[i][j][r]);
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f16x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow, q);
+#pragma unroll
+                    for (int j = 0; j < TI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j][q], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < ntile) store(buf ^ 1);
+        __syncthreads();
+    }
+    w8_store<TI, BT, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+}
+
+// ---- native FP8 kernel: FP8 tiles in LDS, 128-byte rows; 16-byte chunk c of row r sits at
+// chunk c ^ ((r >> 1) & 7) (16 consecutive rows reading one chunk hit 16 distinct bank groups).
+// v_mfma*_16x16x128_f8f6f4 operand layout (measured): lane l holds row l & 15 with
+// k = 16g .. 16g+15 in bytes 0..15 and k = 64 + 16g .. +15 in bytes 16..31 (g = l >> 4), and takes
+// the scale of block b = k / 32 of that row from lane 16b + (l & 15).  So lane l reads chunks g and
+// 4 + g and passes the scale byte of (row l & 15, block g).
+// For FP32 block scales (four v_mfma_f32_16x16x32, lane k-slot 8g + 0..7 each), the 8-byte units
+// of a row are stored transposed (unit k/8 = 4q + g at position 4g + q), so lane group g reads
+// 32 contiguous bytes holding its 8 bytes of blocks q = 0..3.
+template <int FA, int FB, bool UE8M0, int MODE>
+struct W8MxCfg {
+    static constexpr bool F32BLOCK = MODE == W8_BLOCK && !UE8M0;
+    static constexpr int BT = F32BLOCK ? 128 : 256;
+};
+
+template <int FA, int FB, bool UE8M0, int MODE>
+__global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
+                                                    const uint8_t* __restrict__ bt, const void* __restrict__ sb,
+                                                    const float* __restrict__ bias, float* __restrict__ c, int M,
+                                                    int N, int K) {
+    using C = W8MxCfg<FA, FB, UE8M0, MODE>;
+    constexpr int BT = C::BT, TI = BT / 32;
+    constexpr bool F32BLOCK = C::F32BLOCK, BLK = MODE == W8_BLOCK;
+    constexpr int XA = FA == TFP8_E4M3FN ? 0 : 1, XB = FB == TFP8_E4M3FN ? 0 : 1;   // cbsz / blgp codes
+    // UE8M0 scales stay bytes here (the instruction takes them raw): loaded below, not by W8Loader.
+    using L = W8Loader<BT, false, F32BLOCK>;
+    static_assert(!(BLK && UE8M0) || BT == 256, "UE8M0 scale words: one per thread and operand");
+    __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 128];
+    __shared__ __attribute__((aligned(16))) uint32_t sS[2][2][BLK ? BT * (F32BLOCK ? 4 : 1) : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int m0, n0;
+    w8_tile(M, N, BT, m0, n0);
+    L ld(a, sa, bt, sb, M, N, K, m0, n0);
+    const int nkb = K / 32, ntile = (K + 127) / 128;
+
+    // UE8M0 block scales: per step one word per row (bytes = blocks kb0 .. kb0+3).
+    __amdgpu_buffer_rsrc_t rsu[2];
+    uint32_t rsc8[2];
+    if constexpr (BLK && UE8M0) {
+        rsu[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb), (short)0,
+                                                   (int)((uint32_t)min(BT, M - m0) * (uint32_t)nkb), (int)W8_FLAGS);
+        rsu[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb), (short)0,
+                                                   (int)((uint32_t)min(BT, N - n0) * (uint32_t)nkb), (int)W8_FLAGS);
+    }
+    auto load = [&](int kt) {
+        ld.load(kt, tid);
+        if constexpr (BLK && UE8M0) {
+            const int kb0 = kt / 32;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {   // 2 x BT words / 256 threads
+                const int op = i, row = tid;   // BT == 256 words per operand
+                uint32_t v = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t o = kb0 + b < nkb ? (uint32_t)(row * nkb + kb0 + b) : W8_OOB;
+                    v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rsu[op], (int)o, 0, 0) << (8 * b);
+                }
+                rsc8[i] = v;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < L::CH; ++i) {
+                const int ch = tid + i * 256, row = ch >> 3, cc = ch & 7, sw = (row >> 1) & 7;
+                uint8_t* base = &sT[buf][op][row * 128];
+                const uint4 v = ld.rt[op][i];
+                if constexpr (F32BLOCK) {
+                    // units 2cc, 2cc+1 (q = cc >> 1, g = 2 (cc & 1) + 0/1) -> positions 4g + q
+                    const int p0 = 8 * (cc & 1) + (cc >> 1), p1 = p0 + 4;
+                    *(uint2*)(base + 16 * ((p0 >> 1) ^ sw) + 8 * (p0 & 1)) = make_uint2(v.x, v.y);
+                    *(uint2*)(base + 16 * ((p1 >> 1) ^ sw) + 8 * (p1 & 1)) = make_uint2(v.z, v.w);
+                } else {
+                    *(uint4*)(base + 16 * (cc ^ sw)) = v;
+                }
+            }
+        if constexpr (F32BLOCK) {
+#pragma unroll
+            for (int i = 0; i < L::NSW; ++i) {
+                const int w = tid + i * 256;
+                sS[buf][i * 256 / (BT * 4)][w % (BT * 4)] = __float_as_uint(ld.rsc[i]);
+            }
+        } else if constexpr (BLK) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) sS[buf][i][tid] = rsc8[i];
+        }
+    };
+
+    f32x4 acc[TI][TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int frow = lane & 15, g = lane >> 4, sw = (frow >> 1) & 7;
+    // this lane's two 16-byte chunks of a row: (g, 4 + g) for f8f6f4; (2g, 2g+1) for the transposed layout
+    const int c0 = 16 * ((F32BLOCK ? 2 * g : g) ^ sw), c1 = 16 * ((F32BLOCK ? 2 * g + 1 : 4 + g) ^ sw);
+    auto frag = [&](int buf, int op, int row) -> i32x8 {
+        const uint8_t* base = &sT[buf][op][row * 128];
+        const uint4 lo = *(const uint4*)(base + c0), hi = *(const uint4*)(base + c1);
+        return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < ntile; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < ntile) load((t + 1) * 128);
+        i32x8 bf[TI];
+#pragma unroll
+        for (int j = 0; j < TI; ++j) bf[j] = frag(buf, 1, wn * (BT / 2) + j * 16 + frow);
+        if constexpr (F32BLOCK) {
+            float4 sbv[TI];
+#pragma unroll
+            for (int j = 0; j < TI; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * (BT / 2) + j * 16 + frow) * 4];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const i32x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow);
+                float4 sav[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sav[r] = *(const float4*)&sS[buf][0][(wm * (BT / 2) + i * 16 + 4 * g + r) * 4];
+#pragma unroll
+                for (int j = 0; j < TI; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const long av = (long)(uint32_t)af[2 * q] | ((long)(uint32_t)af[2 * q + 1] << 32);
+                        const long bv = (long)(uint32_t)bf[j][2 * q] | ((long)(uint32_t)bf[j][2 * q + 1] << 32);
+                        const f32x4 p = w8_mma<FA, FB>(av, bv, f32x4{0.f, 0.f, 0.f, 0.f});
+                        const float sbq = q == 0 ? sbv[j].x : q == 1 ? sbv[j].y : q == 2 ? sbv[j].z : sbv[j].w;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float saq = q == 0 ? sav[r].x : q == 1 ? sav[r].y : q == 2 ? sav[r].z : sav[r].w;
+                            acc[i][j][r] = fmaf(p[r], saq * sbq, acc[i][j][r]);
+                        }
+                    }
+            }
+        } else {
+            int sbs[TI];
+            if constexpr (BLK) {
+#pragma unroll
+                for (int j = 0; j < TI; ++j) sbs[j] = (int)(sS[buf][1][wn * (BT / 2) + j * 16 + frow] >> (8 * g));
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const i32x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow);
+                if constexpr (BLK) {
+                    const int sas = (int)(sS[buf][0][wm * (BT / 2) + i * 16 + frow] >> (8 * g));
+#pragma unroll
+                    for (int j = 0; j < TI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], acc[i][j], XA, XB, 0,
+                                                                                     sas, 0, sbs[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < TI; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], acc[i][j], XA, XB, 0,
+                                                                                     0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < ntile) store(buf ^ 1);
+        __syncthreads();
+    }
+    w8_store<TI, BT, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+}
+
+template <int FA, int FB, bool UE8M0, int MODE>
+void w8_launch(bool native, const uint8_t* a, const void* sa, const uint8_t* bt, const void* sb, const float* bias,
+               float* c, int M, int N, int K, hipStream_t s) {
+    if (native) {
+        constexpr int BT = W8MxCfg<FA, FB, UE8M0, MODE>::BT;
+        const unsigned grid = (unsigned)(((M + BT - 1) / BT) * ((N + BT - 1) / BT));
+        w8_mx_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
+    } else {
+        const unsigned grid = (unsigned)(((M + 127) / 128) * ((N + 127) / 128));
+        w8_f16_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
+    }
+}
+
+}  // namespace
+
+extern "C" int tfp8_w8a8_quantize(const void* x, int x_dtype, int R, int K, int fmt, int ue8m0, uint8_t* q,
+                                  void* scale, void* stream) {
+    clear_error();
+    if (R < 0 || K < 0 || !valid_fmt(fmt) || !valid_dtype(x_dtype))
+        return fail(TFP8_ERR_ARG, "tfp8_w8a8_quantize: bad R/K/fmt/dtype");
+    if (K % 32) return fail(TFP8_ERR_SHAPE, "tfp8_w8a8_quantize: K=%d must be a multiple of 32", K);
+    if (R == 0 || K == 0) return 0;
+    if (!x || !q || !scale) return fail(TFP8_ERR_ARG, "tfp8_w8a8_quantize: null pointer");
+    if ((uintptr_t)q % 16) return fail(TFP8_ERR_ALIGN, "tfp8_w8a8_quantize: q must be 16-byte aligned");
+    const int64_t blocks = (int64_t)R * (K / 32);
+    const unsigned grid = (unsigned)((blocks + 255) / 256);
+    hipStream_t s = (hipStream_t)stream;
+    TFP8_DISPATCH_FMT(fmt, F, TFP8_DISPATCH_DT(x_dtype, D, {
+        if (ue8m0) w8_quantize_kernel<F, D, true><<<grid, 256, 0, s>>>(x, R, K, q, scale);
+        else w8_quantize_kernel<F, D, false><<<grid, 256, 0, s>>>(x, R, K, q, scale);
+    }));
+    return check_launch("tfp8_w8a8_quantize");
+}
+
+extern "C" int tfp8_w8a8_gemm(const uint8_t* a, int fmt_a, const void* sa, const uint8_t* bt, int fmt_b,
+                              const void* sb, int ue8m0, int mode, int native_fp8, const float* bias, float* c, int M,
+                              int N, int K, void* stream) {
+    clear_error();
+    if (M < 0 || N < 0 || K < 0 || !valid_fmt(fmt_a) || !valid_fmt(fmt_b) || (mode != W8_BLOCK && mode != W8_ROWCOL))
+        return fail(TFP8_ERR_ARG, "tfp8_w8a8_gemm: bad M/N/K/format/mode");
+    if (K % 32) return fail(TFP8_ERR_SHAPE, "tfp8_w8a8_gemm: K=%d must be a multiple of 32", K);
+    if (M == 0 || N == 0) return 0;
+    if (!a || !sa || !bt || !sb || !c) return fail(TFP8_ERR_ARG, "tfp8_w8a8_gemm: null pointer");
+    if ((uintptr_t)a % 16 || (uintptr_t)bt % 16)
+        return fail(TFP8_ERR_ALIGN, "tfp8_w8a8_gemm: A and Bt must be 16-byte aligned");
+    if ((size_t)256 * K >= (1ull << 31)) return fail(TFP8_ERR_SHAPE, "tfp8_w8a8_gemm: K=%d too large", K);
+    hipStream_t s = (hipStream_t)stream;
+#define TFP8_W8(FA_, FB_)                                                                        \
+    {                                                                                            \
+        if (mode == W8_BLOCK) {                                                                  \
+            if (ue8m0) w8_launch<FA_, FB_, true, W8_BLOCK>(native_fp8 != 0, a, sa, bt, sb, bias, c, M, N, K, s);   \
+            else w8_launch<FA_, FB_, false, W8_BLOCK>(native_fp8 != 0, a, sa, bt, sb, bias, c, M, N, K, s);        \
+        } else {                                                                                 \
+            if (ue8m0) w8_launch<FA_, FB_, true, W8_ROWCOL>(native_fp8 != 0, a, sa, bt, sb, bias, c, M, N, K, s);  \
+            else w8_launch<FA_, FB_, false, W8_ROWCOL>(native_fp8 != 0, a, sa, bt, sb, bias, c, M, N, K, s);       \
+        }                                                                                        \
+    }
+    TFP8_DISPATCH_FMT(fmt_a, FA, TFP8_DISPATCH_FMT(fmt_b, FB, TFP8_W8(FA, FB)));
+#undef TFP8_W8
+    return check_launch("tfp8_w8a8_gemm");
+}
+
+}  // namespace tfp8

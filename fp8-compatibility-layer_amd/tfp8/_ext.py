@@ -49,6 +49,8 @@ _SIGS = {
     "tfp8_linear": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),
     "tfp8_gemv": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P]),
     "tfp8_gemm_prepared": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "tfp8_w8a8_quantize": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "tfp8_w8a8_gemm": (_I, [_P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I, _I, _P]),
 }
 
 

@@ -132,6 +132,34 @@ int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, i
                        const float* bias, void* y, int y_dtype, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- W8A8, 32-wide K-block scales
+ * FP8 activations x FP8 weights (reference fp8_cuda.py / fp8_gemm_kernel.cu).
+ *
+ * tfp8_w8a8_quantize replaces fp8_cuda.quantize_k (fp8_cuda.py:74-92): x [R, K] (f16/bf16/f32,
+ * K % 32 == 0) -> q [R, K] FP8 codes (16-byte aligned) and per (row, 32-block) scales [R, K/32]:
+ * s = max(amax / max_finite, 1e-12), f32; or with ue8m0, e = clamp(ceil(log2 s), -127, 127), the
+ * byte e + 127 and s = 2^e.  q = encode(clamp(x / s, +-max_finite)) (round to nearest even).
+ */
+int tfp8_w8a8_quantize(const void* x, int x_dtype, int R, int K, int fmt, int ue8m0, uint8_t* q, void* scale,
+                       void* stream);
+
+/* tfp8_w8a8_gemm replaces the gemm_block_* / gemm_rowcol_* kernels (fp8_gemm_kernel.cu:41-118,
+ * launched by fp8_cuda.fp8_linear, fp8_cuda.py:109-138):
+ *   mode 0 (block):   C[m,n] = sum_kb sa[m,kb] * sb[n,kb] * sum_{k in kb} A[m,k] Bt[n,k] + bias[n]
+ *                     sa [M, K/32], sb [N, K/32]
+ *   mode 1 (row/col): C[m,n] = (sum_k A[m,k] Bt[n,k]) * sa[m] * sb[n] + bias[n];  sa [M], sb [N]
+ * A [M, K] codes in fmt_a, Bt [N, K] codes in fmt_b (the weight transposed: k contiguous); scales
+ * f32, or UE8M0 bytes (255 = NaN) with ue8m0; bias f32 [N] or NULL; C f32 [M, N].  K % 32 == 0;
+ * A and Bt 16-byte aligned.  (The reference requires M, N, K % 32 == 0; any M, N work here.)
+ * native_fp8 = 0: codes decoded to f16 and multiplied on f16 matrix cores, products exact in the
+ *   fp32 sums (the reference's fp16 WMMA numerics; max|C - C64| / max|C64| ~ 1e-7).
+ * native_fp8 = 1: FP8 matrix cores (UE8M0 block scales applied by the MX-scaled instruction);
+ *   those align each dot product's terms to the largest, so ~1e-5 .. 1e-4 of max|C|.
+ */
+int tfp8_w8a8_gemm(const uint8_t* a, int fmt_a, const void* sa, const uint8_t* bt, int fmt_b, const void* sb,
+                   int ue8m0, int mode, int native_fp8, const float* bias, float* c, int M, int N, int K,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif
