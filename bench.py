@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 PEAK_F16_TFLOPS = 2500.0     # MI355X dense fp16/bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense fp8 MFMA
 ROTATE_BYTES = 512 << 20
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_gemv_c2_m1.txt")
 
@@ -188,6 +189,49 @@ def cpu_baseline(q, s, x, bias, G, fmt, nbytes, rounds=5):
                       f"rounds after 2 warm-ups, {med * 1e3:.1f} ms/call"}
 
 
+def bench_w8a8(dev, steps, M=8192, N=8192, K=8192):
+    """fp8_linear's GEMM (tfp8_w8a8_gemm, E4M3 x E4M3, block-32 UE8M0 and FP32 scales) on both
+    matrix-core paths, and its activation quantizer, averaged over `steps` back-to-back launches
+    between events on torch's current stream (same method as the GEMV)."""
+    import torch
+
+    from tfp8 import _ext
+    import fp8_cuda
+    lib = _ext.require()
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M, K, device=dev, generator=g)
+    w = torch.randn(N, K, device=dev, generator=g) * 0.02
+    bias = torch.randn(N, device=dev, generator=g)
+    c = torch.empty(M, N, device=dev)
+    res = {"config": {"workload": f"W8A8 fp8_linear GEMM M={M} N={N} K={K}, E4M3 x E4M3, block-32 scales, "
+                                  f"f32 bias, f32 out"}}
+    fl = 2.0 * M * N * K
+    for ue8m0 in (True, False):
+        a_q, sa = fp8_cuda.quantize_k(x, "e4m3", ue8m0)
+        bt, sb = fp8_cuda.quantize_k(w, "e4m3", ue8m0)
+        for native in (False, True):
+            def call(stream, native=native, a_q=a_q, sa=sa, bt=bt, sb=sb, ue8m0=ue8m0):
+                rc = lib.tfp8_w8a8_gemm(a_q.data_ptr(), 0, sa.data_ptr(), bt.data_ptr(), 0, sb.data_ptr(),
+                                        int(ue8m0), 0, int(native), bias.data_ptr(), c.data_ptr(), M, N, K, stream)
+                if rc:
+                    raise RuntimeError(f"tfp8_w8a8_gemm failed: {_ext.last_error()}")
+            mean = time_layers([call], steps, 3)
+            key = f"{'ue8m0' if ue8m0 else 'f32'}_{'native_fp8' if native else 'exact_f16'}"
+            peak = PEAK_FP8_TFLOPS if native else PEAK_F16_TFLOPS
+            res[key] = {"us": round(mean * 1e6, 1), "tflops": round(fl / mean / 1e12, 1), "peak": peak,
+                        "frac": round(fl / mean / 1e12 / peak, 4)}
+            log(f"[bench] W8A8 {key}: {mean * 1e6:.1f} us -> {fl / mean / 1e12:.1f} TFLOP/s")
+
+    def quant(stream):
+        fp8_cuda.quantize_k(x, "e4m3", True)
+    mq = time_layers([quant], steps, 3)
+    qb = M * K * 4 + M * K + M * K // 32
+    res["quantize_f32"] = {"us": round(mq * 1e6, 1), "gbs": round(qb / mq / 1e9, 1),
+                           "frac": round(qb / mq / 1e9 / PEAK_HBM_GBS, 4)}
+    log(f"[bench] W8A8 quantize {M}x{K} f32 -> E4M3 + UE8M0: {mq * 1e6:.1f} us -> {qb / mq / 1e9:.0f} GB/s")
+    return res
+
+
 def read_traffic():
     """HBM bytes per launch of the GEMV from the committed rocprofv3 --pmc summary, if present."""
     try:
@@ -205,7 +249,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm"], default=None)
+    ap.add_argument("--only", choices=["gemv", "gemm", "w8a8"], default=None)
     ap.add_argument("--sweep", action="store_true", help="also time the C2 decode sweep M=2,4,8 and C3 M=16,64")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run torch copies of a 256 MiB buffer (the known-size kernel that scales the "
@@ -283,6 +327,10 @@ def main():
         out["gemm_sweep"] = gsweep
         del layers
 
+    # ---------------------------------------------------------------- W8A8 block-32 GEMM
+    if a.only in (None, "w8a8"):
+        out["w8a8"] = bench_w8a8(dev, max(10, a.steps // 10))
+
     g = out.get("gemv")
     line = {
         "metric": "M=1 FP8-weight GEMV HBM GB/s (% peak); M=256 fused GEMM TFLOP/s",
@@ -320,6 +368,8 @@ def main():
                                                     "UE8M0, f32 bias, fp16 out", **gm["meta"]}}
         if out.get("gemm_sweep"):
             line["gemm_sweep"] = out["gemm_sweep"]
+    if "w8a8" in out:
+        line["w8a8"] = out["w8a8"]
     line["cpu_baseline"] = out.get("cpu")
     print(json.dumps(line), flush=True)
 
