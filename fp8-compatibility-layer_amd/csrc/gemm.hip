@@ -74,9 +74,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     constexpr int TM = WTM / 16, TN = WTN / 16;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 16x16 MFMA tile");
     static_assert(BK % 32 == 0, "K tile is whole MFMA steps");
-    constexpr int AROW = BK * 2 + 16;               // 16-byte row pad: conflict-free ds_read_b128
+    // Activation tile rows are BK 16-bit values (128 or 256 bytes), unpadded; 16-byte chunk c of
+    // row r sits at chunk c ^ swz(r).  Measured with the LDS bank-conflict counter: a 16-byte row
+    // pad (272-byte rows) costs one extra cycle in every 16-lane pass of the fragment reads, while
+    // this XOR layout is conflict-free for both the reads (16 rows, one chunk each) and the tile
+    // writes (16 lanes per 256-byte row).
+    constexpr int AROW = BK * 2;
     constexpr int BROW = BK + 16;
     constexpr int A_CPR = BK / 8, B_CPR = BK / 16;  // 16-byte chunks per tile row
+    static_assert(A_CPR == 8 || A_CPR == 16, "A tile rows of 128 or 256 bytes");
+    // 256-byte rows: 16 chunks, XOR with row & 15.  128-byte rows: 8 chunks, XOR with
+    // (row >> 1) & 7, so rows r and r + 1 (same chunk index, other half of the banks) and r + 8 differ.
+    auto aswz = [](int row) { return A_CPR == 16 ? (row & 15) : ((row >> 1) & 7); };
     constexpr int A_CHUNKS = BM * A_CPR, B_CHUNKS = BN * B_CPR;
     constexpr int CA = (A_CHUNKS + NT - 1) / NT;
     constexpr int CB = (B_CHUNKS + NT - 1) / NT;
@@ -144,7 +153,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
         for (int i = 0; i < CA; ++i) {
             const int c = tid + i * NT;
             if (A_CHUNKS % NT == 0 || c < A_CHUNKS)
-                *(uint4*)&sA[buf][(c / A_CPR) * AROW + (c % A_CPR) * 16] = ra[slot][i];
+                *(uint4*)&sA[buf][(c / A_CPR) * AROW + (((c % A_CPR) ^ aswz(c / A_CPR)) * 16)] = ra[slot][i];
         }
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
@@ -200,7 +209,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
                 braw[slot][b] = *(const uint2*)&sB[buf][(brow + b * 16) * BROW + ks * 32 + kq];
 #pragma unroll
             for (int a = 0; a < TM; ++a)
-                araw[slot][a] = *(const V*)&sA[buf][(arow + a * 16) * AROW + (ks * 32 + kq) * 2];
+                araw[slot][a] = *(const V*)&sA[buf][(arow + a * 16) * AROW + (((ks * 32 + kq) / 8) ^ aswz(arow)) * 16];
         };
         auto decode = [&](int slot) {
 #pragma unroll
