@@ -9,19 +9,14 @@
 //                                                                      (fp8_gemm_kernel.cu:41-118)
 //
 // The weight operand is taken transposed, Bt[N,K] (k contiguous, as the quantizer writes it):
-// both MFMA operands then load as contiguous k runs.  One v_mfma_f32_16x16x32_{fp8,bf8}_{fp8,bf8}
-// covers one 32-wide block of a 16 x 16 output tile exactly; its fp32 result is multiplied by the
-// row x column scale product and accumulated in fp32 (products of two FP8 values are exact in
-// fp32).  Tiles: 64 x 64 per block of 4 waves (2 x 2, each 32 x 32 = 2 x 2 MFMA tiles), 128-wide
-// K steps staged through registers into a double-buffered LDS pair with the scales of the step.
+// both matrix-core operands then load as contiguous k runs.  The GEMM kernels and their numerics
+// are described at the GEMM section below.
 #include "tfp8_common.h"
 
 namespace tfp8 {
 
 namespace {
 
-constexpr int W8_BM = 64, W8_BN = 64, W8_BK = 128, W8_KB = W8_BK / 32;
-constexpr int W8_ROW = W8_BK + 16;   // LDS row stride (bytes): 16-byte pad
 constexpr uint32_t W8_FLAGS = 0x00020000u;
 constexpr uint32_t W8_OOB = 0x80000000u;
 enum { W8_BLOCK = 0, W8_ROWCOL = 1 };
@@ -112,8 +107,8 @@ __global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict
 //     row/column scales use the unscaled instruction; FP32 block scales use four
 //     v_mfma_f32_16x16x32 per 128-step with the fp32 multiply-accumulate above.
 //
-// Tiling: block tile BT x BT of C, 4 waves in 2 x 2, each owning (BT/2) x (BT/2) = TI x TI MFMA
-// tiles of 16 x 16; K advances 128 per step.  Each step's A and Bt tiles (BT rows x 128 codes,
+// Tiling: block tile BT x BT of C split over a grid of waves, each owning TI x TJ MFMA tiles of
+// 16 x 16; K advances 128 per step.  Each step's A and Bt tiles (BT rows x 128 codes,
 // k contiguous) are loaded into registers one step ahead and written (decoded, for the f16
 // kernel) to the other half of a double-buffered LDS pair, so one barrier per step suffices.
 // Out-of-range rows and the K tail read as zero through buffer-load bounds.
@@ -135,11 +130,12 @@ __device__ __forceinline__ void w8_tile(int M, int N, int BT, int& m0, int& n0) 
 
 // Per-step operand loader: BT rows x 128 codes of A (op 0) and Bt (op 1), CH 16-byte chunks per
 // thread and operand, plus (block mode) the step's 4 scales per row as fp32 words.
-template <int BT, bool UE8M0, bool BLOCK_SCALES>
+template <int BT, bool UE8M0, bool BLOCK_SCALES, int NT = 256>
 struct W8Loader {
-    static constexpr int CH = BT * 8 / 256;
-    static constexpr int NSW = BLOCK_SCALES ? 2 * BT * 4 / 256 : 1;
-    static_assert(BT * 4 % 256 == 0, "scale words of one operand must fill whole thread sweeps");
+    static constexpr int CH = BT * 8 / NT;
+    static constexpr int NSW = BLOCK_SCALES ? 2 * BT * 4 / NT : 1;
+    static_assert(BT * 8 % NT == 0 && (!BLOCK_SCALES || BT * 4 % NT == 0),
+                  "tile chunks and scale words of one operand must fill whole thread sweeps");
     __amdgpu_buffer_rsrc_t rs[2], rss[2];
     int K, nkb;
     uint4 rt[2][CH];
@@ -164,7 +160,7 @@ struct W8Loader {
         for (int op = 0; op < 2; ++op)
 #pragma unroll
             for (int i = 0; i < CH; ++i) {
-                const int ch = tid + i * 256, row = ch >> 3, col = (ch & 7) * 16;
+                const int ch = tid + i * NT, row = ch >> 3, col = (ch & 7) * 16;
                 const uint32_t off = kt + col < K ? (uint32_t)row * (uint32_t)K + (uint32_t)(kt + col) : W8_OOB;
                 rt[op][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)off, 0, 0));
             }
@@ -172,8 +168,8 @@ struct W8Loader {
             const int kb0 = kt / 32;
 #pragma unroll
             for (int i = 0; i < NSW; ++i) {
-                // BT * 4 is a multiple of 256 and tid < 256: the operand depends on i only
-                const int w = tid + i * 256, op = i * 256 / (BT * 4), row = (w >> 2) % BT, q = w & 3;
+                // BT * 4 is a multiple of NT and tid < NT: the operand depends on i only
+                const int w = tid + i * NT, op = i * NT / (BT * 4), row = (w >> 2) % BT, q = w & 3;
                 const bool ok = kb0 + q < nkb;
                 if constexpr (UE8M0) {
                     const uint32_t o = ok ? (uint32_t)(row * nkb + kb0 + q) : W8_OOB;
@@ -187,14 +183,15 @@ struct W8Loader {
     }
 };
 
-// Epilogue: C[m, n] = acc (+ row/column scales) + bias[n], fp32, row-major.
-template <int TI, int BT, bool UE8M0, int MODE>
-__device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TI], const void* sa, const void* sb, const float* bias,
+// Epilogue: C[m, n] = acc (+ row/column scales) + bias[n], fp32, row-major.  The wave owns rows
+// wm * WTM + i * 16 + 4 (lane >> 4) + r and columns wn * WTN + j * 16 + (lane & 15).
+template <int TI, int TJ, int WTM, int WTN, bool UE8M0, int MODE>
+__device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TJ], const void* sa, const void* sb, const float* bias,
                                          float* c, int M, int N, int m0, int n0, int wm, int wn, int lane) {
     const int frow = lane & 15, orow = 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < TI; ++j) {
-        const int n = n0 + wn * (BT / 2) + j * 16 + frow;
+    for (int j = 0; j < TJ; ++j) {
+        const int n = n0 + wn * WTN + j * 16 + frow;
         if (n >= N) continue;
         const float bv = bias ? bias[n] : 0.f;
         const float cs = MODE == W8_ROWCOL ? w8_scale<UE8M0>(sb, (size_t)n) : 1.f;
@@ -202,7 +199,7 @@ __device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TI], const void* sa, c
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * (BT / 2) + i * 16 + orow + r;
+                const int m = m0 + wm * WTM + i * 16 + orow + r;
                 if (m >= M) continue;
                 float v = acc[i][j][r];
                 if constexpr (MODE == W8_ROWCOL) v = v * w8_scale<UE8M0>(sa, (size_t)m) * cs;
@@ -324,7 +321,7 @@ __global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__
         if (t + 1 < ntile) store(buf ^ 1);
         __syncthreads();
     }
-    w8_store<TI, BT, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+    w8_store<TI, TI, BT / 2, BT / 2, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
 // ---- native FP8 kernel: FP8 tiles in LDS, 128-byte rows; 16-byte chunk c of row r sits at
@@ -339,27 +336,36 @@ __global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__
 template <int FA, int FB, bool UE8M0, int MODE>
 struct W8MxCfg {
     static constexpr bool F32BLOCK = MODE == W8_BLOCK && !UE8M0;
+    // FP32 block scales: fp32 multiply-adds on every 32-block partial need the accumulators in
+    // VGPRs, so a 128 x 128 tile of 4 waves.  Row/column scales: 256 x 256 with 8 waves (2 x 4,
+    // two per SIMD, 128 x 64 each), so one wave's LDS and load work overlaps the other's MFMAs
+    // (1.8 PFLOP/s at 8192^3, against 1.6 with 4 waves).  UE8M0 block scales: the scaled MFMA
+    // form needs far more registers than the unscaled one (the same kernel with the scaled form
+    // and constant scales spills 136 VGPRs at 256 registers per wave), so 4 waves, one per SIMD,
+    // with 512 registers each.
     static constexpr int BT = F32BLOCK ? 128 : 256;
+    static constexpr int WM = 2, WN = (MODE == W8_ROWCOL) ? 4 : 2, NT = 64 * WM * WN;
 };
 
 template <int FA, int FB, bool UE8M0, int MODE>
-__global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
-                                                    const uint8_t* __restrict__ bt, const void* __restrict__ sb,
-                                                    const float* __restrict__ bias, float* __restrict__ c, int M,
-                                                    int N, int K) {
+__global__ __attribute__((amdgpu_flat_work_group_size(1, (W8MxCfg<FA, FB, UE8M0, MODE>::NT)))) void w8_mx_kernel(
+    const uint8_t* __restrict__ a, const void* __restrict__ sa, const uint8_t* __restrict__ bt,
+    const void* __restrict__ sb, const float* __restrict__ bias, float* __restrict__ c, int M, int N, int K) {
     using C = W8MxCfg<FA, FB, UE8M0, MODE>;
-    constexpr int BT = C::BT, TI = BT / 32;
+    constexpr int BT = C::BT, WM = C::WM, WN = C::WN, NT = C::NT;
+    constexpr int WTM = BT / WM, WTN = BT / WN, TI = WTM / 16, TJ = WTN / 16;
     constexpr bool F32BLOCK = C::F32BLOCK, BLK = MODE == W8_BLOCK;
     constexpr int XA = FA == TFP8_E4M3FN ? 0 : 1, XB = FB == TFP8_E4M3FN ? 0 : 1;   // cbsz / blgp codes
     // UE8M0 scales stay bytes here (the instruction takes them raw): loaded below, not by W8Loader.
-    using L = W8Loader<BT, false, F32BLOCK>;
-    static_assert(!(BLK && UE8M0) || BT == 256, "UE8M0 scale words: one per thread and operand");
+    using L = W8Loader<BT, false, F32BLOCK, NT>;
+    constexpr int NS8 = 2 * BT / NT;   // UE8M0 scale words (4 blocks of one row) per thread per step
+    static_assert(!(BLK && UE8M0) || (2 * BT) % NT == 0, "UE8M0 scale words fill whole thread sweeps");
     __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 128];
     __shared__ __attribute__((aligned(16))) uint32_t sS[2][2][BLK ? BT * (F32BLOCK ? 4 : 1) : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     int m0, n0;
     w8_tile(M, N, BT, m0, n0);
     L ld(a, sa, bt, sb, M, N, K, m0, n0);
@@ -367,20 +373,23 @@ __global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ 
 
     // UE8M0 block scales: per step one word per row (bytes = blocks kb0 .. kb0+3).
     __amdgpu_buffer_rsrc_t rsu[2];
-    uint32_t rsc8[2];
+    uint32_t rsc8[NS8 > 0 ? NS8 : 1];
     if constexpr (BLK && UE8M0) {
         rsu[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb), (short)0,
                                                    (int)((uint32_t)min(BT, M - m0) * (uint32_t)nkb), (int)W8_FLAGS);
         rsu[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb), (short)0,
                                                    (int)((uint32_t)min(BT, N - n0) * (uint32_t)nkb), (int)W8_FLAGS);
     }
+    // word w = wave * 64 + i * NT + lane of the 2 x BT step words: operand (w / BT) is wave-uniform
+    auto s8_op = [&](int i) { return (wave * 64 + i * NT) / BT; };
+    auto s8_row = [&](int i) { return (wave * 64 + i * NT) % BT + lane; };
     auto load = [&](int kt) {
         ld.load(kt, tid);
         if constexpr (BLK && UE8M0) {
             const int kb0 = kt / 32;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {   // 2 x BT words / 256 threads
-                const int op = i, row = tid;   // BT == 256 words per operand
+            for (int i = 0; i < NS8; ++i) {
+                const int op = s8_op(i), row = s8_row(i);
                 uint32_t v = 0;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
@@ -396,7 +405,7 @@ __global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ 
         for (int op = 0; op < 2; ++op)
 #pragma unroll
             for (int i = 0; i < L::CH; ++i) {
-                const int ch = tid + i * 256, row = ch >> 3, cc = ch & 7, sw = (row >> 1) & 7;
+                const int ch = tid + i * NT, row = ch >> 3, cc = ch & 7, sw = (row >> 1) & 7;
                 uint8_t* base = &sT[buf][op][row * 128];
                 const uint4 v = ld.rt[op][i];
                 if constexpr (F32BLOCK) {
@@ -411,20 +420,20 @@ __global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ 
         if constexpr (F32BLOCK) {
 #pragma unroll
             for (int i = 0; i < L::NSW; ++i) {
-                const int w = tid + i * 256;
-                sS[buf][i * 256 / (BT * 4)][w % (BT * 4)] = __float_as_uint(ld.rsc[i]);
+                const int w = tid + i * NT;
+                sS[buf][i * NT / (BT * 4)][w % (BT * 4)] = __float_as_uint(ld.rsc[i]);
             }
         } else if constexpr (BLK) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) sS[buf][i][tid] = rsc8[i];
+            for (int i = 0; i < NS8; ++i) sS[buf][s8_op(i)][s8_row(i)] = rsc8[i];
         }
     };
 
-    f32x4 acc[TI][TI];
+    f32x4 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int frow = lane & 15, g = lane >> 4, sw = (frow >> 1) & 7;
     // this lane's two 16-byte chunks of a row: (g, 4 + g) for f8f6f4; (2g, 2g+1) for the transposed layout
@@ -441,22 +450,22 @@ __global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ 
     for (int t = 0; t < ntile; ++t) {
         const int buf = t & 1;
         if (t + 1 < ntile) load((t + 1) * 128);
-        i32x8 bf[TI];
-#pragma unroll
-        for (int j = 0; j < TI; ++j) bf[j] = frag(buf, 1, wn * (BT / 2) + j * 16 + frow);
         if constexpr (F32BLOCK) {
-            float4 sbv[TI];
+            i32x8 bf[TJ];
 #pragma unroll
-            for (int j = 0; j < TI; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * (BT / 2) + j * 16 + frow) * 4];
+            for (int j = 0; j < TJ; ++j) bf[j] = frag(buf, 1, wn * WTN + j * 16 + frow);
+            float4 sbv[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * WTN + j * 16 + frow) * 4];
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const i32x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow);
+                const i32x8 af = frag(buf, 0, wm * WTM + i * 16 + frow);
                 float4 sav[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sav[r] = *(const float4*)&sS[buf][0][(wm * (BT / 2) + i * 16 + 4 * g + r) * 4];
+                    sav[r] = *(const float4*)&sS[buf][0][(wm * WTM + i * 16 + 4 * g + r) * 4];
 #pragma unroll
-                for (int j = 0; j < TI; ++j)
+                for (int j = 0; j < TJ; ++j)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const long av = (long)(uint32_t)af[2 * q] | ((long)(uint32_t)af[2 * q + 1] << 32);
@@ -471,41 +480,51 @@ __global__ __launch_bounds__(256) void w8_mx_kernel(const uint8_t* __restrict__ 
                     }
             }
         } else {
-            int sbs[TI];
-            if constexpr (BLK) {
+            // With two waves per SIMD (256 registers per wave) the column tiles go in groups of
+            // JH = 2: only two B fragments and one A fragment are live next to the accumulators,
+            // and each A fragment is read from LDS TJ / JH times.
+            constexpr int JH = NT == 512 && TJ >= 4 ? 2 : TJ;
 #pragma unroll
-                for (int j = 0; j < TI; ++j) sbs[j] = (int)(sS[buf][1][wn * (BT / 2) + j * 16 + frow] >> (8 * g));
-            }
+            for (int jh = 0; jh < TJ; jh += JH) {
+                i32x8 bf[JH];
+                int sbs[JH];
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const i32x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow);
-                if constexpr (BLK) {
-                    const int sas = (int)(sS[buf][0][wm * (BT / 2) + i * 16 + frow] >> (8 * g));
+                for (int j = 0; j < JH; ++j) {
+                    bf[j] = frag(buf, 1, wn * WTN + (jh + j) * 16 + frow);
+                    if constexpr (BLK) sbs[j] = (int)(sS[buf][1][wn * WTN + (jh + j) * 16 + frow] >> (8 * g));
+                }
 #pragma unroll
-                    for (int j = 0; j < TI; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], acc[i][j], XA, XB, 0,
-                                                                                     sas, 0, sbs[j]);
-                } else {
+                for (int i = 0; i < TI; ++i) {
+                    const i32x8 af = frag(buf, 0, wm * WTM + i * 16 + frow);
+                    if constexpr (BLK) {
+                        const int sas = (int)(sS[buf][0][wm * WTM + i * 16 + frow] >> (8 * g));
 #pragma unroll
-                    for (int j = 0; j < TI; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], acc[i][j], XA, XB, 0,
-                                                                                     0, 0, 0);
+                        for (int j = 0; j < JH; ++j)
+                            acc[i][jh + j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                af, bf[j], acc[i][jh + j], XA, XB, 0, sas, 0, sbs[j]);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < JH; ++j)
+                            acc[i][jh + j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                af, bf[j], acc[i][jh + j], XA, XB, 0, 0, 0, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);   // one A fragment live at a time
                 }
             }
         }
         if (t + 1 < ntile) store(buf ^ 1);
         __syncthreads();
     }
-    w8_store<TI, BT, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+    w8_store<TI, TJ, WTM, WTN, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
 template <int FA, int FB, bool UE8M0, int MODE>
 void w8_launch(bool native, const uint8_t* a, const void* sa, const uint8_t* bt, const void* sb, const float* bias,
                float* c, int M, int N, int K, hipStream_t s) {
     if (native) {
-        constexpr int BT = W8MxCfg<FA, FB, UE8M0, MODE>::BT;
-        const unsigned grid = (unsigned)(((M + BT - 1) / BT) * ((N + BT - 1) / BT));
-        w8_mx_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
+        using C = W8MxCfg<FA, FB, UE8M0, MODE>;
+        const unsigned grid = (unsigned)(((M + C::BT - 1) / C::BT) * ((N + C::BT - 1) / C::BT));
+        w8_mx_kernel<FA, FB, UE8M0, MODE><<<grid, C::NT, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
     } else {
         const unsigned grid = (unsigned)(((M + 127) / 128) * ((N + 127) / 128));
         w8_f16_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
