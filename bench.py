@@ -216,7 +216,7 @@ def bench_w8a8(dev, steps, M=8192, N=8192, K=8192):
                 if rc:
                     raise RuntimeError(f"tfp8_w8a8_gemm failed: {_ext.last_error()}")
             mean = time_layers([call], steps, 3)
-            key = f"{'ue8m0' if ue8m0 else 'f32'}_{'native_fp8' if native else 'exact_f16'}"
+            key = f"{'ue8m0' if ue8m0 else 'f32'}_{'native_fp8' if native else 'exact'}"
             peak = PEAK_FP8_TFLOPS if native else PEAK_F16_TFLOPS
             res[key] = {"us": round(mean * 1e6, 1), "tflops": round(fl / mean / 1e12, 1), "peak": peak,
                         "frac": round(fl / mean / 1e12 / peak, 4)}

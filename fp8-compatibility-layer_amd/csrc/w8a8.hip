@@ -92,14 +92,17 @@ __global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict
 }
 
 // ------------------------------------------------------------------ GEMM
-// Two kernels share the tiling below and differ in what the matrix cores multiply:
+// Three kernels share the tiling below and differ in what the matrix cores multiply:
 //
-//   w8_f16_kernel (default): FP8 codes are decoded to f16 once per tile (exact: every FP8 value
-//     is an f16) and multiplied by v_mfma_f32_16x16x32_f16, whose products reach the fp32
-//     accumulator exactly -- the numerics of the reference's fp16 WMMA (fp8_gemm_kernel.cu:72-99).
-//     One MFMA covers exactly one 32-wide scale block of a 16 x 16 tile; in block mode its result
-//     is multiplied by sa * sb and accumulated in fp32 (fp8_gemm_kernel.cu:74-93), in row/column
-//     mode MFMAs accumulate directly and the scales go to the epilogue (:105-113).
+//   w8_bf16_kernel (default for UE8M0 block scales and row/column scales): each FP8 fragment is
+//     decoded to bf16 right before its MFMA with the UE8M0 block scale folded into the decode
+//     (exact), and v_mfma_f32_16x16x32_bf16 accumulates exact products in fp32.
+//   w8_f16_kernel (default for FP32 block scales): FP8 codes are decoded to f16 once per tile
+//     (exact: every FP8 value is an f16) and multiplied by v_mfma_f32_16x16x32_f16, whose products
+//     reach the fp32 accumulator exactly -- the numerics of the reference's fp16 WMMA
+//     (fp8_gemm_kernel.cu:72-99).  One MFMA covers exactly one 32-wide scale block of a 16 x 16
+//     tile; its result is multiplied by sa * sb and accumulated in fp32 (fp8_gemm_kernel.cu:74-93).
+//     Row/column mode accumulates directly and scales in the epilogue (:105-113).
 //   w8_mx_kernel (native FP8): the codes go to the FP8 matrix cores as they are.  Those align
 //     the products of one dot product to the largest and keep about 13 fraction bits (measured:
 //     2^16 + 2^0 sums to 2^16), so results differ from an fp32 sum by ~1e-5..1e-4 of max|C|.
@@ -518,6 +521,141 @@ __global__ __attribute__((amdgpu_flat_work_group_size(1, (W8MxCfg<FA, FB, UE8M0,
     w8_store<TI, TJ, WTM, WTN, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
+// ---- exact kernel with scales folded into the decode: UE8M0 block scales and row/column scales.
+// FP8 tiles stay FP8 in LDS (256 x 256 tile, 8 waves of 128 x 64, two per SIMD, as the native
+// kernel).  Each fragment of one 32-wide block is decoded to bf16 right before its MFMA by
+// v_cvt_scalef32_pk_bf16_{fp8,bf8}, whose scale operand carries an E8M0 exponent: with UE8M0 block
+// scales the lane passes 2^(byte-127) (bits byte << 23), so the bf16 value is code * scale exactly
+// (4 or 3 significant bits, and fp32's exponent range, fit bf16 for every product above 2^-126 --
+// scales from the quantizer are >= 2^-40).  Then v_mfma_f32_16x16x32_bf16 accumulates in fp32
+// with exact products: C = sum_kb sum_k (A sa)(B sb), the reference's per-block sum with the
+// scales moved inside, with no per-block multiply-add.  Row/column scales decode with scale 1 and
+// go to the epilogue.  Lane l of an MFMA for block q reads 8 codes of row l & 15 at
+// k = 32q + 8 (l >> 4) (ds_read_b64 from the XOR-swizzled 128-byte rows).
+template <int F>
+__device__ __forceinline__ uint32_t w8_cvt_bf16(uint32_t w, float scale, bool hi) {
+    bf16x2 v;
+    if constexpr (F == TFP8_E4M3FN)
+        v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, true)
+               : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, false);
+    else
+        v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, scale, true)
+               : __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, scale, false);
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <int F>
+__device__ __forceinline__ bf16x8 w8_frag_bf16(uint2 raw, float scale) {
+    const uint32_t h0 = w8_cvt_bf16<F>(raw.x, scale, false), h1 = w8_cvt_bf16<F>(raw.x, scale, true);
+    const uint32_t h2 = w8_cvt_bf16<F>(raw.y, scale, false), h3 = w8_cvt_bf16<F>(raw.y, scale, true);
+    return __builtin_bit_cast(bf16x8, make_uint4(h0, h1, h2, h3));
+}
+// E8M0 byte q of a scale word, as the f32 whose exponent field is that byte (byte 0 -> 0.0f, whose
+// exponent field 0 is E8M0 2^-127; 255 -> inf, E8M0 NaN).
+__device__ __forceinline__ float w8_e8m0_of(uint32_t word, int q) {
+    return __uint_as_float(((word >> (8 * q)) & 0xFFu) << 23);
+}
+
+template <int FA, int FB, bool UE8M0, int MODE>
+__global__ __launch_bounds__(512) void w8_bf16_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
+                                                      const uint8_t* __restrict__ bt, const void* __restrict__ sb,
+                                                      const float* __restrict__ bias, float* __restrict__ c, int M,
+                                                      int N, int K) {
+    constexpr int BT = 256, WM = 2, WN = 4, NT = 512;
+    constexpr int WTM = BT / WM, WTN = BT / WN, TI = WTM / 16, TJ = WTN / 16;
+    constexpr bool BLK = MODE == W8_BLOCK;
+    static_assert(!BLK || UE8M0, "FP32 block scales cannot be folded into the decode");
+    using L = W8Loader<BT, false, false, NT>;
+    __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 128];
+    __shared__ __attribute__((aligned(16))) uint32_t sS[2][2][BLK ? BT : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int m0, n0;
+    w8_tile(M, N, BT, m0, n0);
+    L ld(a, sa, bt, sb, M, N, K, m0, n0);
+    const int nkb = K / 32, ntile = (K + 127) / 128;
+
+    // UE8M0 block scales: per step one word per row (bytes = blocks kb0 .. kb0+3); 2 x 256 words,
+    // one per thread: waves 0-3 take A's rows, waves 4-7 Bt's (the operand is wave-uniform).
+    __amdgpu_buffer_rsrc_t rsu[2];
+    uint32_t rsc8 = 0;
+    if constexpr (BLK) {
+        rsu[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb), (short)0,
+                                                   (int)((uint32_t)min(BT, M - m0) * (uint32_t)nkb), (int)W8_FLAGS);
+        rsu[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb), (short)0,
+                                                   (int)((uint32_t)min(BT, N - n0) * (uint32_t)nkb), (int)W8_FLAGS);
+    }
+    const int s_op = wave >> 2, s_row = (wave & 3) * 64 + lane;
+    auto load = [&](int kt) {
+        ld.load(kt, tid);
+        if constexpr (BLK) {
+            const int kb0 = kt / 32;
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t o = kb0 + b < nkb ? (uint32_t)(s_row * nkb + kb0 + b) : W8_OOB;
+                v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rsu[s_op], (int)o, 0, 0) << (8 * b);
+            }
+            rsc8 = v;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < L::CH; ++i) {
+                const int ch = tid + i * NT, row = ch >> 3, cc = ch & 7, sw = (row >> 1) & 7;
+                *(uint4*)&sT[buf][op][row * 128 + 16 * (cc ^ sw)] = ld.rt[op][i];
+            }
+        if constexpr (BLK) sS[buf][s_op][s_row] = rsc8;
+    };
+
+    f32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int frow = lane & 15, g = lane >> 4, sw = (frow >> 1) & 7;
+    // 8 codes of block q of a row for this lane: logical chunk 2q + (g >> 1), half g & 1
+    auto raw8 = [&](int buf, int op, int row, int q) -> uint2 {
+        return *(const uint2*)&sT[buf][op][row * 128 + 16 * ((2 * q + (g >> 1)) ^ sw) + 8 * (g & 1)];
+    };
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < ntile; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < ntile) load((t + 1) * 128);
+        uint32_t swa[TI], swb[TJ];   // scale words of this lane's rows and columns
+        if constexpr (BLK) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i) swa[i] = sS[buf][0][wm * WTM + i * 16 + frow];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) swb[j] = sS[buf][1][wn * WTN + j * 16 + frow];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {   // blocks past K hold zero codes (scale byte 0: finite)
+            bf16x8 bd[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                bd[j] = w8_frag_bf16<FB>(raw8(buf, 1, wn * WTN + j * 16 + frow, q), BLK ? w8_e8m0_of(swb[j], q) : 1.f);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const bf16x8 ad =
+                    w8_frag_bf16<FA>(raw8(buf, 0, wm * WTM + i * 16 + frow, q), BLK ? w8_e8m0_of(swa[i], q) : 1.f);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, bd[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (t + 1 < ntile) store(buf ^ 1);
+        __syncthreads();
+    }
+    w8_store<TI, TJ, WTM, WTN, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+}
+
 template <int FA, int FB, bool UE8M0, int MODE>
 void w8_launch(bool native, const uint8_t* a, const void* sa, const uint8_t* bt, const void* sb, const float* bias,
                float* c, int M, int N, int K, hipStream_t s) {
@@ -525,7 +663,12 @@ void w8_launch(bool native, const uint8_t* a, const void* sa, const uint8_t* bt,
         using C = W8MxCfg<FA, FB, UE8M0, MODE>;
         const unsigned grid = (unsigned)(((M + C::BT - 1) / C::BT) * ((N + C::BT - 1) / C::BT));
         w8_mx_kernel<FA, FB, UE8M0, MODE><<<grid, C::NT, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
-    } else {
+        return;
+    }
+    if constexpr (MODE == W8_ROWCOL || UE8M0) {   // scales fold into the decode or the epilogue
+        const unsigned grid = (unsigned)(((M + 255) / 256) * ((N + 255) / 256));
+        w8_bf16_kernel<FA, FB, UE8M0, MODE><<<grid, 512, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
+    } else {                                       // FP32 block scales: per-block multiply-add
         const unsigned grid = (unsigned)(((M + 127) / 128) * ((N + 127) / 128));
         w8_f16_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
     }
