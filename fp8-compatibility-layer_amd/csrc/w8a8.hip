@@ -102,7 +102,6 @@ __global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict
 //     reach the fp32 accumulator exactly -- the numerics of the reference's fp16 WMMA
 //     (fp8_gemm_kernel.cu:72-99).  One MFMA covers exactly one 32-wide scale block of a 16 x 16
 //     tile; its result is multiplied by sa * sb and accumulated in fp32 (fp8_gemm_kernel.cu:74-93).
-//     Row/column mode accumulates directly and scales in the epilogue (:105-113).
 //   w8_mx_kernel (native FP8): the codes go to the FP8 matrix cores as they are.  Those align
 //     the products of one dot product to the largest and keep about 13 fraction bits (measured:
 //     2^16 + 2^0 sums to 2^16), so results differ from an fp32 sum by ~1e-5..1e-4 of max|C|.
@@ -211,20 +210,21 @@ __device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TJ], const void* sa, c
     }
 }
 
-// ---- exact kernel: f16 tiles in LDS.  A row of a tile is 128 halves = 16 chunks of 8; chunk u
-// (k = 8u .. 8u+7) of row r sits at chunk u ^ (r & 15), so the 16 rows read by one ds_read_b128
-// of a fragment land on 16 distinct 4-bank groups.  Lane l of an MFMA for scale block q reads
-// row l & 15, chunk 4q + (l >> 4): k = 32q + 8 (l >> 4) + 0..7, the instruction's own k order.
-template <int FA, int FB, bool UE8M0, int MODE>
-__global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
-                                                     const uint8_t* __restrict__ bt, const void* __restrict__ sb,
+// ---- exact kernel for FP32 block scales: f16 tiles in LDS.  A row of a tile is 128 halves = 16
+// chunks of 8; chunk u (k = 8u .. 8u+7) of row r sits at chunk u ^ (r & 15), so the 16 rows read by
+// one ds_read_b128 of a fragment land on 16 distinct 4-bank groups.  Lane l of an MFMA for scale
+// block q reads row l & 15, chunk 4q + (l >> 4): k = 32q + 8 (l >> 4) + 0..7, the instruction's own
+// k order.  Each MFMA result (one 32-block of a 16 x 16 tile) is multiplied by sa * sb and added to
+// the fp32 accumulator (fp8_gemm_kernel.cu:74-93).
+template <int FA, int FB>
+__global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__ a, const float* __restrict__ sa,
+                                                     const uint8_t* __restrict__ bt, const float* __restrict__ sb,
                                                      const float* __restrict__ bias, float* __restrict__ c, int M,
                                                      int N, int K) {
     constexpr int BT = 128, TI = BT / 32;
-    constexpr bool BLK = MODE == W8_BLOCK;
-    using L = W8Loader<BT, UE8M0, BLK>;
-    __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 256];       // [buffer][A, Bt][row * 256 B]
-    __shared__ __attribute__((aligned(16))) float sS[2][2][BLK ? BT * 4 : 1];  // [buffer][A, Bt][row * 4 + q]
+    using L = W8Loader<BT, false, true>;
+    __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 256];   // [buffer][A, Bt][row * 256 B]
+    __shared__ __attribute__((aligned(16))) float sS[2][2][BT * 4];       // [buffer][A, Bt][row * 4 + q]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -252,12 +252,10 @@ __global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__
                 *(uint4*)(base + 16 * ((2 * cc) ^ sw)) = make_uint4(h[0], h[1], h[2], h[3]);
                 *(uint4*)(base + 16 * ((2 * cc + 1) ^ sw)) = make_uint4(h[4], h[5], h[6], h[7]);
             }
-        if constexpr (BLK) {
 #pragma unroll
-            for (int i = 0; i < L::NSW; ++i) {
-                const int w = tid + i * 256;
-                sS[buf][i * 256 / (BT * 4)][w % (BT * 4)] = ld.rsc[i];
-            }
+        for (int i = 0; i < L::NSW; ++i) {
+            const int w = tid + i * 256;
+            sS[buf][i * 256 / (BT * 4)][w % (BT * 4)] = ld.rsc[i];
         }
     };
 
@@ -283,48 +281,35 @@ __global__ __launch_bounds__(256) void w8_f16_kernel(const uint8_t* __restrict__
         for (int j = 0; j < TI; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) bf[j][q] = frag(buf, 1, wn * (BT / 2) + j * 16 + frow, q);
-        if constexpr (BLK) {
-            float4 sbv[TI];
+        float4 sbv[TI];
 #pragma unroll
-            for (int j = 0; j < TI; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * (BT / 2) + j * 16 + frow) * 4];
+        for (int j = 0; j < TI; ++j) sbv[j] = *(const float4*)&sS[buf][1][(wn * (BT / 2) + j * 16 + frow) * 4];
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                f16x8 af[4];
+        for (int i = 0; i < TI; ++i) {
+            f16x8 af[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) af[q] = frag(buf, 0, wm * (BT / 2) + i * 16 + frow, q);
-                float4 sav[4];
+            for (int q = 0; q < 4; ++q) af[q] = frag(buf, 0, wm * (BT / 2) + i * 16 + frow, q);
+            float4 sav[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sav[r] = *(const float4*)&sS[buf][0][(wm * (BT / 2) + i * 16 + 4 * g + r) * 4];
+            for (int r = 0; r < 4; ++r) sav[r] = *(const float4*)&sS[buf][0][(wm * (BT / 2) + i * 16 + 4 * g + r) * 4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {   // blocks past K hold zero codes and finite scales
+            for (int q = 0; q < 4; ++q) {   // blocks past K hold zero codes and zero scales
 #pragma unroll
-                    for (int j = 0; j < TI; ++j) {
-                        const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q], bf[j][q], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        const float sbq = q == 0 ? sbv[j].x : q == 1 ? sbv[j].y : q == 2 ? sbv[j].z : sbv[j].w;
+                for (int j = 0; j < TI; ++j) {
+                    const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q], bf[j][q], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const float sbq = q == 0 ? sbv[j].x : q == 1 ? sbv[j].y : q == 2 ? sbv[j].z : sbv[j].w;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float saq = q == 0 ? sav[r].x : q == 1 ? sav[r].y : q == 2 ? sav[r].z : sav[r].w;
-                            acc[i][j][r] = fmaf(p[r], saq * sbq, acc[i][j][r]);
-                        }
+                    for (int r = 0; r < 4; ++r) {
+                        const float saq = q == 0 ? sav[r].x : q == 1 ? sav[r].y : q == 2 ? sav[r].z : sav[r].w;
+                        acc[i][j][r] = fmaf(p[r], saq * sbq, acc[i][j][r]);
                     }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f16x8 af = frag(buf, 0, wm * (BT / 2) + i * 16 + frow, q);
-#pragma unroll
-                    for (int j = 0; j < TI; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j][q], acc[i][j], 0, 0, 0);
                 }
             }
         }
         if (t + 1 < ntile) store(buf ^ 1);
         __syncthreads();
     }
-    w8_store<TI, TI, BT / 2, BT / 2, UE8M0, MODE>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
+    w8_store<TI, TI, BT / 2, BT / 2, false, W8_BLOCK>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
 // ---- native FP8 kernel: FP8 tiles in LDS, 128-byte rows; 16-byte chunk c of row r sits at
@@ -670,7 +655,7 @@ void w8_launch(bool native, const uint8_t* a, const void* sa, const uint8_t* bt,
         w8_bf16_kernel<FA, FB, UE8M0, MODE><<<grid, 512, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
     } else {                                       // FP32 block scales: per-block multiply-add
         const unsigned grid = (unsigned)(((M + 127) / 128) * ((N + 127) / 128));
-        w8_f16_kernel<FA, FB, UE8M0, MODE><<<grid, 256, 0, s>>>(a, sa, bt, sb, bias, c, M, N, K);
+        w8_f16_kernel<FA, FB><<<grid, 256, 0, s>>>(a, (const float*)sa, bt, (const float*)sb, bias, c, M, N, K);
     }
 }
 

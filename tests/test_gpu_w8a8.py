@@ -118,6 +118,30 @@ def test_large_against_torch_float64(ue8m0, native):
     assert rel < (NATIVE_TOL if native else 1e-5), rel
 
 
+@pytest.mark.parametrize("native", [False, True])
+@pytest.mark.parametrize("ue8m0", [False, True])
+def test_format_pairs_and_nan_scale(native, ue8m0):
+    """A=E5M2 x B=E4M3 (the pair the host test does not run), and a NaN scale (UE8M0 byte 255,
+    fp8_gemm_kernel.cu:8, or an f32 NaN) on one (row, block) of A: that output row is NaN, the
+    others are unaffected."""
+    M, N, K = 96, 80, 288
+    print(f"[w8a8] e5m2 x e4m3 + NaN scale native={native} ue8m0={ue8m0}", flush=True)
+    x, w, bias = W.host_case_data(M, N, K, seed=11)
+    a, sa = W.quantize_k(x, "e5m2", ue8m0)
+    bt, sb = W.quantize_k(w.T.copy(), "e4m3", ue8m0)
+    ref = W.gemm_ref(a, "e5m2", sa, bt, "e4m3", sb, ue8m0, 0, bias)
+    tol = NATIVE_TOL if native else 1e-5
+    c = _gemm(_cuda(a), "e5m2", _cuda(sa), _cuda(bt), "e4m3", _cuda(sb), ue8m0, 0, _cuda(bias), M, N, K, native)
+    assert W.rel_err(c.cpu().numpy(), ref) < tol
+    sa_nan = sa.copy()
+    sa_nan[7, 3] = 255 if ue8m0 else np.float32(np.nan)
+    c = _gemm(_cuda(a), "e5m2", _cuda(sa_nan), _cuda(bt), "e4m3", _cuda(sb), ue8m0, 0, _cuda(bias), M, N, K,
+              native).cpu().numpy()
+    assert np.isnan(c[7]).all()
+    keep = np.arange(M) != 7
+    assert W.rel_err(c[keep], ref[keep]) < tol
+
+
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("ue8m0", [False, True])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
