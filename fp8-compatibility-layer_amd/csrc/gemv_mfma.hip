@@ -12,10 +12,13 @@
 //     second kernel runs; each wave covers all NT row tiles, so one activation fragment feeds NT
 //     weight tiles (every load instruction costs the same address-unit time whether it brings
 //     weights or activations, so fewer activation loads per weight byte is what matters);
-//   * lane l handles weight row l & 15 and the 16-byte k slot l >> 4 of every 64-byte chunk, so
-//     one buffer_load_dwordx4 reads 16 rows x 64 bytes; its low and high 8 codes are the B
-//     operands of two MFMAs, and the activation operands are the same k positions of activation
-//     row l & 15, loaded from L2 (two 16-byte loads per chunk; rows past M read zeros);
+//   * lane l handles weight row l & 15 and the 16-byte k slot l >> 4 of every 64-byte chunk; the low
+//     and high 8 codes of those 16 bytes are the B operands of two MFMAs, and the activation
+//     operands are the same k positions of activation row l & 15, loaded from L2 (two 16-byte loads
+//     per chunk; rows past M read zeros).  The weights are not loaded in that layout (16 rows x 64
+//     bytes per load streams ~15 % slower than 256 contiguous bytes per row): a group of 4 chunks
+//     arrives as 4 loads of 4 rows x 256 bytes, goes through a wave-private LDS tile and is read
+//     back as operands (when every wave's K range is whole groups; else the direct layout);
 //   * D chunks per wave are in flight; every load is unconditional (out-of-range rows, chunks and
 //     the k tail read zeros through the buffer resources);
 //   * scales: per channel in the epilogue; K-group scales of the block's rows are staged in LDS
@@ -65,7 +68,7 @@ __device__ __forceinline__ uint4 gv_load16(__amdgpu_buffer_rsrc_t r, uint32_t of
                : __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-template <typename T, int FMT, int SMODE, int NT, int W, int D>
+template <typename T, int FMT, int SMODE, int NT, int W, int D, bool TL>
 __global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__ x, const float* __restrict__ xs,
                                                            const uint8_t* __restrict__ w, const void* __restrict__ ws,
                                                            int sk, const float* __restrict__ bias,
@@ -94,16 +97,35 @@ __global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__
     const uint32_t wlane = (uint32_t)j * (uint32_t)K + (uint32_t)q * 16u;
     const uint32_t xlane = ((uint32_t)j * (uint32_t)K + (uint32_t)q * 16u) * (uint32_t)sizeof(T);
 
+    // Weight loads.  Direct layout (TL = false): load t of chunk c is the MFMA operand itself, 16 rows
+    // x 64 bytes (lane l: row l & 15, 16 bytes at slot l >> 4).  Transposed layout (TL = true): the
+    // 4 chunks of a 256-code group are 4 loads of 4 rows x 256 contiguous bytes each (lane l: row
+    // 4a + (l >> 4), 16 bytes at l & 15), which stream from HBM ~15 % faster than 64-byte pieces of
+    // 16 rows; the wave writes them to its own LDS tile and reads the operands back (LDS operations
+    // of one wave complete in order, so no barrier).  TL processes D / 4 groups in flight.
     uint4 wb[D][NT], xa[D], xb[D];
     auto issue = [&](int d, int c) {
         const int k = c * 64 + q * 16;
         const bool ok = c < c1 && k < K;
+        if constexpr (TL) {
+            // d = 4 * group slot + a; c is the group's first chunk + a.  Load a of the group: rows
+            // 4a .. 4a+3, bytes 64 * (c - a) .. +256 of each.
+            const int a4 = d & 3, cg = c - a4;
+            const int kk = cg * 64 + j * 16;
+            const bool okg = cg < c1 && kk < K;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-            wb[d][t] = gv_load16(wr, ok ? wlane + (uint32_t)(t * 16) * (uint32_t)K + (uint32_t)c * 64u : GM_OOB, 1);
+            for (int t = 0; t < NT; ++t)
+                wb[d][t] = gv_load16(wr, okg ? (uint32_t)(t * 16 + 4 * a4 + q) * (uint32_t)K + (uint32_t)kk : GM_OOB, 1);
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                wb[d][t] = gv_load16(wr, ok ? wlane + (uint32_t)(t * 16) * (uint32_t)K + (uint32_t)c * 64u : GM_OOB, 1);
+        }
         xa[d] = gv_load16(xr, ok ? xlane + (uint32_t)c * 64u * (uint32_t)sizeof(T) : GM_OOB, 0);
         xb[d] = gv_load16(xr, ok ? xlane + ((uint32_t)c * 64u + 8u) * (uint32_t)sizeof(T) : GM_OOB, 0);
     };
+    // TL: this wave's transpose tiles, NT x [16 rows][256 bytes], 16-byte unit u of row r at u ^ r.
+    uint8_t* tls = smem + sbytes + W * NT * 64 * sizeof(f32x4) + (size_t)wave * NT * 4096;
 
     // Weight and activation loads of the first D chunks go out before the scales are staged.
 #pragma unroll
@@ -128,12 +150,25 @@ __global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__
     auto compute = [&](int d, int c) {
         const int k = c * 64 + q * 16;
         const int g = min(gshift >= 0 ? (k >> gshift) : k / G, ng - 1);
+        if constexpr (TL) {
+            if ((d & 3) == 0) {
+                // The group's 4 loads (rows 4a + q, 16-byte unit j) into this wave's tiles.
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const int r = 4 * a4 + q;
+                        *(uint4*)(tls + t * 4096 + r * 256 + 16 * (j ^ r)) = wb[d + a4][t];
+                    }
+            }
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int srow = min(t * 16 + j, rows - 1);
             float s = 1.f;
             if constexpr (SMODE == SM_UE8M0) s = ue8m0_to_f32(smem[srow * ng + g]);
-            const uint4 wv = wb[d][t];
+            // operand of chunk c: row j, 16-byte unit 4 (c mod 4) + q of the group
+            const uint4 wv = TL ? *(const uint4*)(tls + t * 4096 + j * 256 + 16 * ((4 * (d & 3) + q) ^ j)) : wb[d][t];
             uint4 lo, hi;
             lo.x = Op::template cvt<FMT>(wv.x, s, false);
             lo.y = Op::template cvt<FMT>(wv.x, s, true);
@@ -195,11 +230,18 @@ __global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__
 
 template <typename T, int FMT, int SMODE, int NT, int W, int D>
 static void gm_launch(const void* x, const float* xs, const uint8_t* w, const void* ws, int sk, const float* bias,
-                      void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int sbytes, hipStream_t s) {
+                      void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int sbytes, bool tl,
+                      hipStream_t s) {
     const unsigned grid = (unsigned)((N + 16 * NT - 1) / (16 * NT));
-    const size_t lds = (size_t)sbytes + (size_t)W * NT * 64 * sizeof(f32x4);
-    gemv_mfma_kernel<T, FMT, SMODE, NT, W, D><<<grid, 64 * W, lds, s>>>((const T*)x, xs, w, ws, sk, bias, y, ydt, M,
-                                                                         N, K, G, ng, gshift, sbytes);
+    const size_t lds = (size_t)sbytes + (size_t)W * NT * 64 * sizeof(f32x4) + (tl ? (size_t)W * NT * 4096 : 0);
+    if (tl) {
+        if constexpr (D % 4 == 0)
+            gemv_mfma_kernel<T, FMT, SMODE, NT, W, D, true><<<grid, 64 * W, lds, s>>>(
+                (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes);
+    } else {
+        gemv_mfma_kernel<T, FMT, SMODE, NT, W, D, false><<<grid, 64 * W, lds, s>>>(
+            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes);
+    }
 }
 
 static int gm_env_int(const char* name, int dflt) {
@@ -210,17 +252,17 @@ static int gm_env_int(const char* name, int dflt) {
 template <typename T, int FMT, int SMODE>
 static void gm_pick(int NT, int W, int D, const void* x, const float* xs, const uint8_t* w, const void* ws, int sk,
                     const float* bias, void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int sbytes,
-                    hipStream_t s) {
+                    bool tl, hipStream_t s) {
 #define TFP8_GM_CFG(NT_, W_, D_)                                                                                   \
     if (NT == NT_ && W == W_ && D == D_) {                                                                       \
-        gm_launch<T, FMT, SMODE, NT_, W_, D_>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, s); \
+        gm_launch<T, FMT, SMODE, NT_, W_, D_>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, tl, s); \
         return;                                                                                                  \
     }
     TFP8_GM_CFG(2, 8, 4) TFP8_GM_CFG(2, 8, 8) TFP8_GM_CFG(2, 4, 4) TFP8_GM_CFG(2, 4, 8)
     TFP8_GM_CFG(1, 8, 4) TFP8_GM_CFG(1, 8, 8) TFP8_GM_CFG(1, 4, 4) TFP8_GM_CFG(1, 4, 8)
     TFP8_GM_CFG(4, 4, 4) TFP8_GM_CFG(4, 8, 4) TFP8_GM_CFG(4, 4, 2) TFP8_GM_CFG(2, 4, 2)
 #undef TFP8_GM_CFG
-    gm_launch<T, FMT, SMODE, 2, 8, 4>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, s);
+    gm_launch<T, FMT, SMODE, 2, 4, 4>(x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, false, s);
 }
 
 }  // namespace
@@ -239,12 +281,16 @@ int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, con
     // (sweep on MI355X at C2 M=4/8; TFP8_GM_NT / _W / _D override, for tuning).
     const int NT = gm_env_int("TFP8_GM_NT", 2), W = gm_env_int("TFP8_GM_W", 4), D = gm_env_int("TFP8_GM_D", 4);
     const int sbytes = sm == SM_CHANNEL ? 0 : (16 * NT * ng * (sm == SM_F32 ? 4 : 1) + 15) / 16 * 16;
-    if (sbytes + W * NT * 1024 > 64 * 1024) return 1;   // scales of the block's rows too large for LDS
+    // Transposed weight loads (C2 M=4: 18.1 -> 15.0 us, M=8: 19.4 -> 15.4 us; identical results)
+    // need whole 256-code groups in every wave's K range; TFP8_GM_TL=0 keeps the direct layout.
+    bool tl = gm_env_int("TFP8_GM_TL", 1) != 0 && D % 4 == 0 && K % (256 * W) == 0;
+    if (tl && sbytes + W * NT * (1024 + 4096) > 64 * 1024) tl = false;   // transpose tiles do not fit
+    if (sbytes + W * NT * 1024 > 64 * 1024) return 1;                      // scales of the block's rows
 #define TFP8_GM_SM(T_, F_)                                                                                    \
     {                                                                                                         \
-        if (sm == SM_CHANNEL) gm_pick<T_, F_, SM_CHANNEL>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, s); \
-        else if (sm == SM_UE8M0) gm_pick<T_, F_, SM_UE8M0>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, s); \
-        else gm_pick<T_, F_, SM_F32>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, s); \
+        if (sm == SM_CHANNEL) gm_pick<T_, F_, SM_CHANNEL>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, tl, s); \
+        else if (sm == SM_UE8M0) gm_pick<T_, F_, SM_UE8M0>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, tl, s); \
+        else gm_pick<T_, F_, SM_F32>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, tl, s); \
     }
     if (x_dtype == TFP8_BF16) {
         TFP8_DISPATCH_FMT(fmt, F, TFP8_GM_SM(__bf16, F));

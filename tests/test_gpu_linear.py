@@ -348,3 +348,24 @@ def test_decode_mfma_every_config(nt, w, d, monkeypatch):
     _run(5, 200, 1152, 64, torch.float16, xdt=torch.float16, seed=nt + w + d)
     _run(8, 136, 544, 32, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", bias=False, seed=d)  # tail 32
     _run(3, 40, 96, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=w)
+    # K a multiple of 256 x W: the transposed weight-load layout (rows past N in the last block)
+    _run(6, 72, 256 * w * 2, 128, torch.bfloat16, xdt=torch.bfloat16, seed=w * d)
+    _run(4, 40, 256 * w, None, torch.float16, fmt="e5m2", xdt=torch.float16, sf="ue8m0", seed=nt)
+
+
+@pytest.mark.parametrize("M,N,K,G,sf", [(4, 14336, 4096, 128, "f32"), (8, 4096, 4096, None, "ue8m0"),
+                                        (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32")])
+def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
+    """The decode kernel's transposed weight loads (4 rows x 256 bytes per load, regrouped through
+    LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
+    64 bytes per load): the outputs must be bit-identical."""
+    print(f"[linear] decode transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
+    q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).bfloat16().cuda()
+    outs = []
+    for tl in ("0", "1"):
+        monkeypatch.setenv("TFP8_GM_TL", tl)
+        outs.append(_ext.w8a16(x, q, None, s, b, torch.bfloat16, GG, "e4m3fn"))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    _check(outs[1], x, q, s, GG, "e4m3fn", b, torch.bfloat16, "gemv", "decode transposed loads")
