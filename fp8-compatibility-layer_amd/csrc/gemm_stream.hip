@@ -6,10 +6,12 @@
 //   * a block is 4 waves over a 64*NW-row slice of W (each wave owns NW 16-row MFMA tiles) and all
 //     M rows (TM 16-row MFMA tiles), and one K slice (split-K over gridDim.y when the tile grid is
 //     too small for 256 CUs; fp32 partials then go to the caller's workspace);
-//   * weights are read with buffer_load_dwordx4 (non-temporal) straight into registers: lane l
-//     reads 16 consecutive codes of row (l & 15) at k = 64c + 16(l >> 4), so one instruction covers
-//     16 rows x 64 bytes, and its low/high 8 codes are the B operands of two
-//     v_mfma_f32_16x16x32_{f16,bf16} (the activation operand reads the same permuted k order);
+//   * weights are read with buffer_load_dwordx4 (non-temporal): the MFMA B operand of lane l is 16
+//     consecutive codes of row (l & 15) at k = 64c + 16(l >> 4), whose low/high 8 codes feed two
+//     v_mfma_f32_16x16x32_{f16,bf16} (the activation operand reads the same permuted k order).
+//     With 256-code chunks the loads are 4 rows x 256 contiguous bytes each (16 rows x 64 bytes per
+//     instruction streams ~15 % slower) and each wave regroups them through its own LDS tile;
+//     shorter chunks load the operand layout directly;
 //     a whole chunk of KCS*64 k for all NW tiles is in flight while the previous chunk is consumed;
 //   * codes are decoded in registers with v_cvt_scalef32_pk_{f16,bf16}_{fp8,bf8}; UE8M0 K-group
 //     scales ride in that instruction's scale operand (it multiplies by the scale's power of two,
@@ -59,7 +61,7 @@ enum { GM_CHANNEL = 0, GM_UE8M0 = 1, GM_F32 = 2 };
 
 }  // namespace
 
-template <typename T, int FMT, int TM, int NW, int KCS, int GMODE>
+template <typename T, int FMT, int TM, int NW, int KCS, int GMODE, bool TL>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(
     const T* __restrict__ x, const float* __restrict__ xs, const uint8_t* __restrict__ w, const void* __restrict__ ws,
     int sk, const float* __restrict__ bias, void* __restrict__ y, int ydt, int M, int N, int K, int G, int ng,
@@ -72,6 +74,9 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(
     constexpr int XPIECES = XROWS * KC / 8;      // 16-byte pieces per chunk
     constexpr int XPT = (XPIECES + 255) / 256;   // pieces per thread
     __shared__ __attribute__((aligned(16))) uint8_t sx[2][XROWS * ROWB];
+    // TL: each wave's weight tiles regrouped, NW x [16 rows][256 bytes], 16-byte unit u of row r at u ^ r
+    static_assert(!TL || KCS == 4, "transposed loads take a 256-code chunk");
+    __shared__ __attribute__((aligned(16))) uint8_t wt[TL ? 4 * NW * 4096 : 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -103,8 +108,17 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(
             const bool ok = chunk < nchunks && kk < (uint32_t)kend;
 #pragma unroll
             for (int j = 0; j < NW; ++j) {
-                const uint32_t off = ok ? roff[j] + kk : oob;
-                buf[st][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)off, 0, GS_NT));
+                if constexpr (TL) {
+                    // load st of the chunk: rows 4 st .. 4 st + 3 of the tile, 256 contiguous bytes each
+                    const int row = nb + j * 16 + 4 * st + (lane >> 4);
+                    const uint32_t k2 = (uint32_t)k0 + 16u * (uint32_t)(lane & 15);
+                    const bool ok2 = chunk < nchunks && k2 < (uint32_t)kend && row < N;
+                    const uint32_t off = ok2 ? (uint32_t)row * (uint32_t)K + k2 : oob;
+                    buf[st][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)off, 0, GS_NT));
+                } else {
+                    const uint32_t off = ok ? roff[j] + kk : oob;
+                    buf[st][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)off, 0, GS_NT));
+                }
                 if constexpr (GMODE != GM_CHANNEL) {
                     const int n = min(nb + j * 16 + (lane & 15), N - 1);
                     const int g = ok ? (gshift >= 0 ? (int)(kk >> gshift) : (int)kk / G) : 0;
@@ -145,22 +159,37 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(
 #pragma unroll
         for (int j = 0; j < NW; ++j) acc[a][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    uint8_t* wtile = &wt[TL ? wave * NW * 4096 : 0];
     auto compute = [&](const uint4 (&buf)[KCS][NW], const float (&sv)[GMODE == GM_CHANNEL ? 1 : KCS][NW], int xb) {
+        if constexpr (TL) {
+            // The chunk's loads into this wave's tiles (LDS operations of one wave complete in order).
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+#pragma unroll
+                for (int st = 0; st < KCS; ++st) {
+                    const int r = 4 * st + (lane >> 4);
+                    *(uint4*)(wtile + j * 4096 + r * 256 + 16 * ((lane & 15) ^ r)) = buf[st][j];
+                }
+        }
 #pragma unroll
         for (int st = 0; st < KCS; ++st) {
             V b1[NW], b2[NW];
 #pragma unroll
             for (int j = 0; j < NW; ++j) {
                 const float s = GMODE == GM_UE8M0 ? sv[st][j] : 1.f;
+                // operand of step st: row lane & 15, 16-byte unit 4 st + (lane >> 4)
+                const uint4 wv = TL ? *(const uint4*)(wtile + j * 4096 + (lane & 15) * 256 +
+                                                      16 * ((4 * st + (lane >> 4)) ^ (lane & 15)))
+                                    : buf[st][j];
                 uint4 d1, d2;
-                d1.x = Op::template cvt<FMT>(buf[st][j].x, s, false);
-                d1.y = Op::template cvt<FMT>(buf[st][j].x, s, true);
-                d1.z = Op::template cvt<FMT>(buf[st][j].y, s, false);
-                d1.w = Op::template cvt<FMT>(buf[st][j].y, s, true);
-                d2.x = Op::template cvt<FMT>(buf[st][j].z, s, false);
-                d2.y = Op::template cvt<FMT>(buf[st][j].z, s, true);
-                d2.z = Op::template cvt<FMT>(buf[st][j].w, s, false);
-                d2.w = Op::template cvt<FMT>(buf[st][j].w, s, true);
+                d1.x = Op::template cvt<FMT>(wv.x, s, false);
+                d1.y = Op::template cvt<FMT>(wv.x, s, true);
+                d1.z = Op::template cvt<FMT>(wv.y, s, false);
+                d1.w = Op::template cvt<FMT>(wv.y, s, true);
+                d2.x = Op::template cvt<FMT>(wv.z, s, false);
+                d2.y = Op::template cvt<FMT>(wv.z, s, true);
+                d2.z = Op::template cvt<FMT>(wv.w, s, false);
+                d2.w = Op::template cvt<FMT>(wv.w, s, true);
                 b1[j] = __builtin_bit_cast(V, d1);
                 b2[j] = __builtin_bit_cast(V, d2);
             }
@@ -316,8 +345,17 @@ static void gs_launch(int slices, int slice_len, const void* x, const float* xs,
                       hipStream_t s) {
     dim3 grid((N + 64 * NW - 1) / (64 * NW), slices);
     const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
-    gemm_stream_kernel<T, FMT, TM, NW, KCS, GMODE><<<grid, 256, 0, s>>>((const T*)x, xs, w, ws, sk, bias, y, ydt, M, N,
-                                                                       K, G, ng, gshift, part, slice_len, N);
+    // 256-code chunks load as 4 rows x 256 contiguous bytes per instruction and are regrouped in LDS
+    // (TFP8_GS_TL=0 keeps the 16 rows x 64 bytes operand layout).
+    if constexpr (KCS == 4) {
+        if (gs_env_int("TFP8_GS_TL", 1)) {
+            gemm_stream_kernel<T, FMT, TM, NW, KCS, GMODE, true><<<grid, 256, 0, s>>>(
+                (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, part, slice_len, N);
+            return;
+        }
+    }
+    gemm_stream_kernel<T, FMT, TM, NW, KCS, GMODE, false><<<grid, 256, 0, s>>>((const T*)x, xs, w, ws, sk, bias, y, ydt,
+                                                                              M, N, K, G, ng, gshift, part, slice_len, N);
 }
 
 template <typename T, int FMT, int GMODE>

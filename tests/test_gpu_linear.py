@@ -353,6 +353,24 @@ def test_decode_mfma_every_config(nt, w, d, monkeypatch):
     _run(4, 40, 256 * w, None, torch.float16, fmt="e5m2", xdt=torch.float16, sf="ue8m0", seed=nt)
 
 
+@pytest.mark.parametrize("M,N,K,G,sf", [(16, 8192, 8192, None, "ue8m0"), (24, 1000, 2048, 128, "f32"),
+                                        (32, 520, 4096, 32, "ue8m0"), (13, 300, 832, 64, "f32")])
+def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
+    """The weight-streaming GEMM's transposed weight loads (256-code chunks as 4 rows x 256 bytes,
+    regrouped through LDS) against its direct operand-layout loads: bit-identical outputs (same
+    operands, same order), including the K tail, rows past N and split-K."""
+    print(f"[linear] stream transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
+    q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().cuda()
+    outs = []
+    for tl in ("0", "1"):
+        monkeypatch.setenv("TFP8_GS_TL", tl)
+        outs.append(_ext.w8a16(x, q, None, s, b, torch.float16, GG, "e4m3fn"))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    _check(outs[1], x, q, s, GG, "e4m3fn", b, torch.float16, "gemm", "stream transposed loads")
+
+
 @pytest.mark.parametrize("M,N,K,G,sf", [(4, 14336, 4096, 128, "f32"), (8, 4096, 4096, None, "ue8m0"),
                                         (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32")])
 def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
