@@ -455,6 +455,7 @@ GemmPlan gemm_plan(int M, int N, int K, bool grouped) {
 }
 
 size_t gemm_stream_partial_bytes(int M, int N, int K, int G, int ws_kind);
+size_t gemm_direct_partial_bytes(int M, int N, int K);
 
 // Workspace for either GEMM kernel's split-K partials (the streaming kernel's split is sized
 // with per-channel alignment, an upper bound for every group size).
@@ -462,7 +463,7 @@ size_t gemm_partial_bytes(int M, int N, int K) {
     const GemmPlan p = gemm_plan(M, N, K, false), q = gemm_plan(M, N, K, true);
     const int sl = std::max(p.slices, q.slices);
     const size_t v1 = sl > 1 ? (size_t)sl * M * N * sizeof(float) : 0;
-    return std::max(v1, gemm_stream_partial_bytes(M, N, K, K, TFP8_SCALE_F32));
+    return std::max({v1, gemm_stream_partial_bytes(M, N, K, K, TFP8_SCALE_F32), gemm_direct_partial_bytes(M, N, K)});
 }
 
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
@@ -487,6 +488,9 @@ void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws
 }
 
 int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
+                    const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
+                    float* partial, hipStream_t s);
+int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
                     const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
                     float* partial, hipStream_t s);
 int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, const uint8_t* w, int N, const void* ws,
@@ -548,6 +552,8 @@ int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, cons
     }
     const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
     if (rs != 1) return rs;
+    const int rd = run_gemm_direct(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
+    if (rd != 1) return rd;
     const int ng = K / G;
     GemmPlan p = gemm_plan(M, N, K, ng > 1);
     int slices = p.slices, slice_len = K;

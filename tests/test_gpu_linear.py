@@ -296,6 +296,7 @@ def test_tiled_gemm_every_config(tile, monkeypatch):
     without split-K, on ragged shapes: rows past M and N, a K tail that is not a whole K tile,
     per-channel and K-group (f32 G=32, UE8M0 G=64) scales, f16 and bf16 activations."""
     monkeypatch.setenv("TFP8_GEMM_V1", "1")
+    monkeypatch.setenv("TFP8_GEMM_DIRECT", "0")
     monkeypatch.setenv("TFP8_GEMM_TILE", str(tile))
     for split in (1, 3):
         monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
@@ -304,11 +305,13 @@ def test_tiled_gemm_every_config(tile, monkeypatch):
         _run(257, 136, 704, 64, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", seed=tile + 2)
 
 
-def test_split_k_workspace_contents_do_not_matter(monkeypatch):
+@pytest.mark.parametrize("direct", ["0", "1"])
+def test_split_k_workspace_contents_do_not_matter(direct, monkeypatch):
     """Split-K through the caller's workspace (fp32 partial tiles, then the reduce kernel): a
     workspace full of garbage, or one reused from the previous call, gives the same bits every
-    time, within the oracle tolerance."""
+    time, within the oracle tolerance (LDS-tiled kernel and direct-load kernel)."""
     monkeypatch.setenv("TFP8_GEMM_V1", "1")
+    monkeypatch.setenv("TFP8_GEMM_DIRECT", direct)
     monkeypatch.setenv("TFP8_GEMM_TILE", "13")
     monkeypatch.setenv("TFP8_GEMM_SPLITK", "3")
     lib = _ext.require()
@@ -332,6 +335,37 @@ def test_split_k_workspace_contents_do_not_matter(monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     _check(outs[0], x, q, s, G, "e4m3fn", b, torch.float16, "gemm", "split-K arrival")
+
+
+@pytest.mark.parametrize("M,N,K,xdt,out,fmt,sf,bias,split", [
+    (129, 256, 64, torch.float16, torch.float16, "e4m3fn", "ue8m0", True, 0),     # one K step, 1 row past 128
+    (200, 300, 128, torch.bfloat16, torch.bfloat16, "e5m2", "f32", False, 0),     # two steps, ragged N
+    (136, 72, 192, torch.float16, torch.float32, "e4m3fn", "f32", True, 0),       # three steps, N < one tile
+    (256, 1000, 2048, torch.float16, torch.float32, "e4m3fn", "f32", True, 0),
+    (384, 512, 4096, torch.bfloat16, torch.bfloat16, "e4m3fn", "ue8m0", True, 3),  # uneven split (1408, 1408, 1280)
+    (1000, 2048, 1024, torch.float16, torch.float16, "e5m2", "ue8m0", True, 1),
+    (300, 512, 512, torch.float32, torch.float32, "e4m3fn", "f32", True, 2),      # fp32 x: f16 prep + row scales
+])
+def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, monkeypatch):
+    """The direct-load GEMM (M > 128, one scale per weight row): rows past M and N inside a tile,
+    K of one to three steps (fewer than the LDS ring holds), even and uneven split-K, f16 / bf16 /
+    fp32 activations, both formats, f32 and UE8M0 scales, every output dtype."""
+    if split:
+        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+    _run(M, N, K, None, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=M + K)
+
+
+@pytest.mark.parametrize("stages,wn,ra", [("3", "4", "1"), ("5", "4", "1"), ("4", "2", "1"), ("4", "4", "0"),
+                                           ("4", "2", "0"), ("5", "2", "0")])
+def test_direct_gemm_variants(stages, wn, ra, monkeypatch):
+    """The non-default instantiations of the direct-load GEMM: 3- and 5-stage LDS rings (default
+    4), 4 waves of 64 x 128 (default 8 of 64 x 64), fragments read half a K step ahead (default a
+    whole step), on short and long K slices."""
+    monkeypatch.setenv("TFP8_GEMM_STAGES", stages)
+    monkeypatch.setenv("TFP8_GEMM_WN", wn)
+    monkeypatch.setenv("TFP8_GEMM_RA", ra)
+    _run(130, 520, 128, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=3)
+    _run(256, 768, 3072, None, torch.bfloat16, xdt=torch.bfloat16, seed=4)
 
 
 @pytest.mark.parametrize("nt,w,d", [(2, 8, 4), (2, 8, 8), (2, 4, 4), (2, 4, 8), (1, 8, 4), (1, 8, 8), (1, 4, 4), (1, 4, 8)])
