@@ -544,16 +544,17 @@ static int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } retu
 int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
              const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, float* partial,
              hipStream_t s) {
-    // Decode sizes go to the matrix-core decode kernel (no split-K), then the weight-streaming
-    // kernel (which is as fast from 9 rows up); the LDS-tiled kernel below is the general path.
+    // Decode sizes go to the matrix-core decode kernel (no split-K); then the direct-to-LDS GEMM
+    // (one scale per weight row, from its minimum M up), the weight-streaming kernel (M <= 128)
+    // and the LDS-tiled kernel below, the general path.
     if (M <= 8 && M >= gemv_mfma_min_m()) {
         const int rm = run_gemv_mfma(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rm != 1) return rm;
     }
-    const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
-    if (rs != 1) return rs;
     const int rd = run_gemm_direct(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
     if (rd != 1) return rd;
+    const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
+    if (rs != 1) return rs;
     const int ng = K / G;
     GemmPlan p = gemm_plan(M, N, K, ng > 1);
     int slices = p.slices, slice_len = K;

@@ -1,15 +1,14 @@
-// FP8-weight GEMM for many activation rows (M > 128) with one scale per weight row, on gfx950.
+// FP8-weight GEMM for many activation rows (M > 64) with one scale per weight row, on gfx950.
 //
 // y[m,n] = xs[m] * s[n] * sum_k x[m,k] * decode(w[n,k]) + bias[n]
 // (reference gemm_w8a16, tfp8/csrc/tfp8_kernels.cu:271-411, per-channel / per-tensor case; the
 // reference's chunked path, tfp8/linear.py:107-128, computes the same product).  Built around
 // gfx950 measurements:
-//   * buffer_load ... lds moves a K step's activation tile (f16/bf16, 128 x 64) and raw FP8 weight
-//     tile (256 x 64) straight into LDS, no VGPR staging and no ds_write; the steps form a ring of
-//     S buffers, loads issued S-1 steps ahead, one barrier per K step;
-//   * v_mfma_f32_32x32x16_{f16,bf16}: the 128 x 256 block tile is 8 waves of 64 x 64 (two per
-//     SIMD, so one wave's waits are covered by the other's MFMAs; WN = 2 gives 4 waves of
-//     64 x 128 instead);
+//   * buffer_load ... lds moves a K step's activation tile (f16/bf16, BM x 64) and raw FP8 weight
+//     tile (BN x 64) straight into LDS, no VGPR staging and no ds_write; the steps form a ring of
+//     S buffers (up to 160 KB), loads issued S-1 steps ahead, one barrier per K step;
+//   * v_mfma_f32_32x32x16_{f16,bf16}; at M = 256 the 128 x 256 block tile is 8 waves of 64 x 64
+//     (two per SIMD, so one wave's waits are covered by the other's MFMAs);
 //   * ds_read_b128 moves about twice the bytes per clock of ds_read_b64, so a lane reads 16 codes
 //     of a weight row at once.  Inside each 32-wide K window, lane half h (lane >> 5) holds
 //     k = 16h .. 16h+15: codes 0-7 feed one MFMA and codes 8-15 the next, and the activation
@@ -31,10 +30,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_void_t;
 
 constexpr uint32_t GD_BUF_FLAGS = 0x00020000u;   // buffer resource word 3 (raw, 32-bit format)
-constexpr int GD_BM = 128, GD_BN = 256, GD_BK = 64;
-constexpr int GD_ABYTES = GD_BM * GD_BK * 2;       // activation tile: 128 rows x 128 bytes
-constexpr int GD_BBYTES = GD_BN * GD_BK;           // weight tile: 256 rows x 64 codes
-constexpr int GD_STAGE = GD_ABYTES + GD_BBYTES;    // 32 KB per ring stage
+constexpr int GD_BK = 64;                          // K step: 128-byte activation rows, 64-byte weight rows
+constexpr int GD_LDS_MAX = 160 * 1024;             // LDS per workgroup on gfx950
 
 template <typename T> struct GdOp;
 template <> struct GdOp<_Float16> {
@@ -76,33 +73,38 @@ __device__ __forceinline__ void gd_load_lds(__amdgpu_buffer_rsrc_t rsrc, uint32_
 }
 
 // Waits until at most `stages` stages of this wave's loads (L load instructions each) are
-// outstanding, stages in 0..3.
+// outstanding, stages in 0..5.
 template <int L>
 __device__ __forceinline__ void gd_wait_vm(int stages) {
-    static_assert(L == 4 || L == 8, "4 or 8 loads per stage");
+    static_assert(L >= 1 && 5 * L <= 63, "vmcnt holds at most 63");
     switch (stages) {
         case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
         case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory"); break;
         case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory"); break;
-        default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * L) : "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * L) : "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * L) : "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * L) : "memory"); break;
     }
 }
 
-// WN = 2: 4 waves (one per SIMD) of 64 x 128; WN = 4: 8 waves (two per SIMD) of 64 x 64.
-template <typename T, int FMT, int S, int WN, int RA>
-__global__ __launch_bounds__(128 * WN) void gemm_direct_kernel(
+// Block tile BM x BN (BM = 32, 64 or 128 activation rows; BN = 128 or 256 weight rows), WM x WN
+// waves, ring of S K steps.
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     const T* __restrict__ x, const float* __restrict__ xs, const uint8_t* __restrict__ w,
     const void* __restrict__ ws, int sk, const float* __restrict__ bias, void* __restrict__ y, int ydt,
     int M, int N, int K, float* __restrict__ part, int slice_len) {
     using Op = GdOp<T>;
     typedef typename Op::V V;
-    constexpr int NT = 128 * WN, NW = NT / 64;
-    constexpr int TM = 2, TN = 8 / WN;       // 32 x 32 MFMA tiles per wave
-    constexpr int WTN = GD_BN / WN;          // wave tile columns
-    constexpr int LA = 16 / NW;              // 1 KB activation (and weight) loads per wave per stage
-    static_assert(WN == 2 || WN == 4, "wave grid 2 x 2 or 2 x 4");
-    static_assert(S >= 3 && S <= 5, "ring of 3 to 5 stages (160 KB of LDS at most)");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * GD_STAGE];
+    constexpr int NW = WM * WN;
+    constexpr int WTM = BM / WM, WTN = BN / WN;     // wave tile
+    constexpr int TM = WTM / 32, TN = WTN / 32;     // 32 x 32 MFMA tiles per wave
+    constexpr int ABYTES = BM * GD_BK * 2, STAGE = ABYTES + BN * GD_BK;
+    constexpr int LA = BM / 8 / NW, LB = BN / 16 / NW;   // 1 KB loads per wave per stage
+    static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile of whole 32x32 MFMA tiles");
+    static_assert(LA >= 1 && LB >= 1 && LA * NW * 8 == BM && LB * NW * 16 == BN, "loads split evenly over waves");
+    static_assert(S >= 3 && S <= 7 && S * STAGE <= GD_LDS_MAX, "ring of 3 to 7 stages in 160 KB of LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -111,53 +113,57 @@ __global__ __launch_bounds__(128 * WN) void gemm_direct_kernel(
 
     // XCD-aware tile order: consecutive ids land on one XCD and walk M first, so the blocks that
     // read one weight tile share an L2.
-    const int ntm = (M + GD_BM - 1) / GD_BM, ntn = (N + GD_BN - 1) / GD_BN, nt = ntm * ntn;
+    const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN, nt = ntm * ntn;
     int id = blockIdx.x;
     if ((nt & 7) == 0) id = (blockIdx.x & 7) * (nt >> 3) + (blockIdx.x >> 3);
-    const int m0 = (id % ntm) * GD_BM, n0 = (id / ntm) * GD_BN;
+    const int m0 = (id % ntm) * BM, n0 = (id / ntm) * BN;
     const int kbeg = blockIdx.y * slice_len;
     const int nst = min(slice_len, K - kbeg) / GD_BK;   // whole K steps (K % 64 == 0, checked on the host)
 
     // Rows past M / N are out of range of these resources; whatever they leave in LDS only reaches
     // output rows / columns that are never stored.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(x + (size_t)m0 * K), (short)0, (int)((uint32_t)min(GD_BM, M - m0) * (uint32_t)K * 2u), (int)GD_BUF_FLAGS);
+        (void*)(x + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * (uint32_t)K * 2u), (int)GD_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(w + (size_t)n0 * K), (short)0, (int)((uint32_t)min(GD_BN, N - n0) * (uint32_t)K), (int)GD_BUF_FLAGS);
+        (void*)(w + (size_t)n0 * K), (short)0, (int)((uint32_t)min(BN, N - n0) * (uint32_t)K), (int)GD_BUF_FLAGS);
 
     // LDS layouts (16-byte units): activation row r (128 B) keeps chunk c at c ^ ((r >> 1) & 7),
     // weight row r (64 B) keeps chunk c at c ^ ((r >> 2) & 3); both make the 16-row fragment
     // reads below conflict-free.  A load instruction fills 1 KB of LDS in lane order, so lane j of
     // instruction i fetches the global chunk that belongs at unit 64 i + j.
-    uint32_t aoff[LA], boff[LA];
+    uint32_t aoff[LA], boff[LB];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int u = (wave * LA + i) * 64 + lane;
         const int ar = u >> 3, ac = (u & 7) ^ ((ar >> 1) & 7);
         aoff[i] = (uint32_t)ar * (uint32_t)K * 2u + (uint32_t)ac * 16u;
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+        const int u = (wave * LB + i) * 64 + lane;
         const int br = u >> 2, bc = (u & 3) ^ ((br >> 2) & 3);
         boff[i] = (uint32_t)br * (uint32_t)K + (uint32_t)bc * 16u;
     }
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t)smem + (uint32_t)wave * (LA * 1024u);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t)smem;
     auto issue = [&](int st) {
-        const uint32_t sa = lds0 + (uint32_t)(st % S) * GD_STAGE;
+        const uint32_t sa = lds0 + (uint32_t)(st % S) * STAGE;
         const uint32_t kk = (uint32_t)(kbeg + st * GD_BK);
 #pragma unroll
-        for (int i = 0; i < LA; ++i) gd_load_lds(ra, sa + i * 1024, aoff[i], kk * 2u);
+        for (int i = 0; i < LA; ++i) gd_load_lds(ra, sa + (wave * LA + i) * 1024, aoff[i], kk * 2u);
 #pragma unroll
-        for (int i = 0; i < LA; ++i) gd_load_lds(rb, sa + GD_ABYTES + i * 1024, boff[i], kk);
+        for (int i = 0; i < LB; ++i) gd_load_lds(rb, sa + ABYTES + (wave * LB + i) * 1024, boff[i], kk);
     };
 
     // Fragment offsets inside a stage.  Window p (k = 32p .. 32p+31 of the step), half q:
-    // activation chunk 4p + 2h + q of row wm*64 + tm*32 + l32; weight chunk 2p + h of row
+    // activation chunk 4p + 2h + q of row wm*WTM + tm*32 + l32; weight chunk 2p + h of row
     // wn*WTN + tn*32 + l32 (16 codes: q = 0 uses the first 8, q = 1 the last 8).
     const int aswz = (l32 >> 1) & 7, bswz = (l32 >> 2) & 3;
     uint32_t a_rd[2][2], b_rd[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) a_rd[p][q] = (uint32_t)(wm * 64 + l32) * 128u + 16u * (uint32_t)((4 * p + 2 * h + q) ^ aswz);
-        b_rd[p] = GD_ABYTES + (uint32_t)(wn * WTN + l32) * 64u + 16u * (uint32_t)((2 * p + h) ^ bswz);
+        for (int q = 0; q < 2; ++q) a_rd[p][q] = (uint32_t)(wm * WTM + l32) * 128u + 16u * (uint32_t)((4 * p + 2 * h + q) ^ aswz);
+        b_rd[p] = ABYTES + (uint32_t)(wn * WTN + l32) * 64u + 16u * (uint32_t)((2 * p + h) ^ bswz);
     }
 
     f32x16 acc[TM][TN];
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(128 * WN) void gemm_direct_kernel(
         uint4 b[TN];
     };
     auto read = [&](int st, int p, Frag& f) {
-        const uint8_t* base = smem + (st % S) * GD_STAGE;
+        const uint8_t* base = smem + (st % S) * STAGE;
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) f.b[tn] = *(const uint4*)(base + b_rd[p] + tn * 2048);
 #pragma unroll
@@ -194,55 +200,40 @@ __global__ __launch_bounds__(128 * WN) void gemm_direct_kernel(
     // Stage st is complete in LDS for every wave once each wave has waited for its own loads of it
     // (stages up to `last` have been issued; loads complete in order) and all have passed the barrier.
     auto sync_stage = [&](int st, int last) {
-        gd_wait_vm<2 * LA>(last - st);
+        gd_wait_vm<LA + LB>(last - st);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
 
-    // Pipeline: K steps 0..S-2 are loaded up front; in step t the first K window multiplies while
-    // the second is read from LDS, then (after the barrier that also retires step t-1's buffer)
-    // step t+S-1 is issued into that buffer and the second window multiplies while step t+1's
-    // first window is read.
+    // Pipeline: K steps 0..S-2 are loaded up front.  Step t+1 is published at the top of step t
+    // (the same barrier retires step t-1's buffer, into which step t+S-1 is then issued), and both
+    // K windows of step t+1 are read from LDS while step t multiplies: two register sets, swapped
+    // by unrolling the loop by two.
     for (int st = 0; st < S - 1 && st < nst; ++st) issue(st);
-    Frag f0, f1;
+    Frag f0, f1, g0, g1;
     sync_stage(0, min(nst - 1, S - 2));
     read(0, 0, f0);
-    if constexpr (RA == 0) {
-        for (int t = 0; t < nst; ++t) {
-            read(t, 1, f1);
-            mma(f0);
-            if (t + 1 < nst) sync_stage(t + 1, min(nst - 1, t + S - 2));
-            if (t + S - 1 < nst) issue(t + S - 1);
-            if (t + 1 < nst) read(t + 1, 0, f0);
-            mma(f1);
-        }
-    } else {
-        // Fragments one whole K step ahead: step t+1 is published at the top of step t and both
-        // of its windows are read while step t multiplies (two register sets, swapped by
-        // unrolling the loop by two).
-        Frag g0, g1;
-        read(0, 1, f1);
-        auto step = [&](int t, Frag& c0, Frag& c1, Frag& n0, Frag& n1) {
-            const bool more = t + 1 < nst;
-            if (more) sync_stage(t + 1, min(nst - 1, t + S - 2));
-            if (t + S - 1 < nst) issue(t + S - 1);
-            if (more) read(t + 1, 0, n0);
-            mma(c0);
-            if (more) read(t + 1, 1, n1);
-            mma(c1);
-        };
-        int t = 0;
-        for (; t + 1 < nst; t += 2) {
-            step(t, f0, f1, g0, g1);
-            step(t + 1, g0, g1, f0, f1);
-        }
-        if (t < nst) step(t, f0, f1, g0, g1);
+    read(0, 1, f1);
+    auto step = [&](int t, Frag& c0, Frag& c1, Frag& n0, Frag& n1) {
+        const bool more = t + 1 < nst;
+        if (more) sync_stage(t + 1, min(nst - 1, t + S - 2));
+        if (t + S - 1 < nst) issue(t + S - 1);
+        if (more) read(t + 1, 0, n0);
+        mma(c0);
+        if (more) read(t + 1, 1, n1);
+        mma(c1);
+    };
+    int t = 0;
+    for (; t + 1 < nst; t += 2) {
+        step(t, f0, f1, g0, g1);
+        step(t + 1, g0, g1, f0, f1);
     }
+    if (t < nst) step(t, f0, f1, g0, g1);
 
     // Epilogue.  32x32 MFMA output layout: lane l holds column l & 31 and rows
     // 8 (i >> 2) + 4 (l >> 5) + (i & 3) of accumulator element i.
-    const int rbase = m0 + wm * 64 + 4 * h;
+    const int rbase = m0 + wm * WTM + 4 * h;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
         const int col = n0 + wn * WTN + tn * 32 + l32;
@@ -281,12 +272,46 @@ int gd_env_int(const char* name, int dflt) {
 
 }  // namespace
 
-// Whether this kernel takes the shape, and its split of K (slices of whole 64-wide steps; a block
-// per CU for the 256 CUs, slices of at least 1024).
+namespace {
+
+// Launch configurations: block tile, wave grid, ring depth.
+struct GdCfg {
+    int bm, bn, wm, wn, stages;
+};
+constexpr GdCfg GD_CFGS[] = {
+    {128, 256, 2, 4, 4},   // 0: M > 128 (C3 M=256), 8 waves of 64 x 64
+    {128, 256, 2, 2, 4},   // 1: 4 waves of 64 x 128
+    {128, 256, 2, 4, 3},   // 2
+    {128, 256, 2, 4, 5},   // 3
+    {64, 256, 2, 4, 6},    // 4: M <= 64, 8 waves of 32 x 64
+    {32, 256, 1, 4, 7},    // 5: M <= 32, 4 waves of 32 x 64
+    {128, 128, 2, 4, 6},   // 6: 8 waves of 64 x 32
+    {64, 128, 2, 2, 7},    // 7: 4 waves of 32 x 64
+};
+constexpr int GD_NCFG = (int)(sizeof(GD_CFGS) / sizeof(GD_CFGS[0]));
+
+// Smallest M this kernel takes; the weight-streaming kernel serves fewer rows.  Sweep on MI355X
+// at K = N = 8192 (us, weight-streaming vs this kernel's best configuration): M=16 17.2 vs 22.9,
+// M=32 22.0 vs 24.7, M=64 27.5 vs 26.4, M=128 43.4 vs 33.3 (128 x 128, 6 stages), M=256 56.1
+// (LDS-tiled) vs 50.7 (128 x 256, 4 stages).
+int gd_min_m() { return gd_env_int("TFP8_GEMM_DIRECT_MIN_M", 65); }
+
+GdCfg gd_cfg(int M) {
+    int c = M > 128 ? 0 : M > 64 ? 6 : M > 32 ? 7 : 5;
+    const int f = gd_env_int("TFP8_GEMM_DCFG", -1);   // tuning hook: index into GD_CFGS
+    if (f >= 0 && f < GD_NCFG) c = f;
+    return GD_CFGS[c];
+}
+
+}  // namespace
+
+// Whether this kernel takes the shape, and its split of K (slices of whole 64-wide steps until
+// the grid has a block per CU, slices of at least 1024).
 bool gemm_direct_plan(int M, int N, int K, int G, int* slices, int* slice_len) {
-    if (G != K || K % GD_BK != 0 || M <= 128 || !gd_env_int("TFP8_GEMM_DIRECT", 1)) return false;
-    if ((long)GD_BN * K >= (1L << 31) || (long)GD_BM * K * 2 >= (1L << 31)) return false;
-    const long tiles = (long)((M + GD_BM - 1) / GD_BM) * ((N + GD_BN - 1) / GD_BN);
+    if (G != K || K % GD_BK != 0 || M < gd_min_m() || !gd_env_int("TFP8_GEMM_DIRECT", 1)) return false;
+    const GdCfg c = gd_cfg(M);
+    if ((long)c.bn * K >= (1L << 31) || (long)c.bm * K * 2 >= (1L << 31)) return false;
+    const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     int s = 1;
     while (tiles * s < 256 && s < 8 && K / (s * 2) >= 1024) s *= 2;
     const int fs = gd_env_int("TFP8_GEMM_SPLITK", 0);
@@ -310,28 +335,22 @@ void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws
 template <typename T, int FMT>
 static void gd_launch(int slices, int slice_len, const void* x, const float* xs, const uint8_t* w, const void* ws,
                       int sk, const float* bias, void* y, int ydt, int M, int N, int K, float* part, hipStream_t s) {
-    const int nt = ((M + GD_BM - 1) / GD_BM) * ((N + GD_BN - 1) / GD_BN);
-    dim3 grid(nt, slices);
-    // Tuning hooks (defaults from a sweep on MI355X at M = 256, K = N = 8192): ring depth 3-5,
-    // 4 or 8 waves, fragments read one K step (1) or half a step (0) ahead.
-    const int stages = gd_env_int("TFP8_GEMM_STAGES", 4), wn = gd_env_int("TFP8_GEMM_WN", 4);
-    const int ra = gd_env_int("TFP8_GEMM_RA", 1);
-#define GD_K(S_, WN_)                                                                                         \
-    do {                                                                                                      \
-        if (ra) gemm_direct_kernel<T, FMT, S_, WN_, 1><<<grid, 128 * WN_, 0, s>>>(                            \
-            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, part, slice_len);                              \
-        else gemm_direct_kernel<T, FMT, S_, WN_, 0><<<grid, 128 * WN_, 0, s>>>(                               \
-            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, part, slice_len);                              \
-    } while (0)
-    if (wn == 4) {
-        if (stages == 5) GD_K(5, 4);
-        else if (stages == 3) GD_K(3, 4);
-        else GD_K(4, 4);
-    } else {
-        if (stages == 5) GD_K(5, 2);
-        else if (stages == 3) GD_K(3, 2);
-        else GD_K(4, 2);
+    const GdCfg c = gd_cfg(M);
+    const dim3 grid(((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn), slices);
+#define GD_K(BM_, BN_, WM_, WN_, S_)                                                                           \
+    if (c.bm == BM_ && c.bn == BN_ && c.wm == WM_ && c.wn == WN_ && c.stages == S_) {                          \
+        gemm_direct_kernel<T, FMT, BM_, BN_, WM_, WN_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(                    \
+            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, part, slice_len);                               \
+        return;                                                                                                \
     }
+    GD_K(128, 256, 2, 4, 4)
+    GD_K(128, 256, 2, 2, 4)
+    GD_K(128, 256, 2, 4, 3)
+    GD_K(128, 256, 2, 4, 5)
+    GD_K(64, 256, 2, 4, 6)
+    GD_K(32, 256, 1, 4, 7)
+    GD_K(128, 128, 2, 4, 6)
+    GD_K(64, 128, 2, 2, 7)
 #undef GD_K
 }
 

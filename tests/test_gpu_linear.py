@@ -355,17 +355,16 @@ def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, monkeypatch
     _run(M, N, K, None, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=M + K)
 
 
-@pytest.mark.parametrize("stages,wn,ra", [("3", "4", "1"), ("5", "4", "1"), ("4", "2", "1"), ("4", "4", "0"),
-                                           ("4", "2", "0"), ("5", "2", "0")])
-def test_direct_gemm_variants(stages, wn, ra, monkeypatch):
-    """The non-default instantiations of the direct-load GEMM: 3- and 5-stage LDS rings (default
-    4), 4 waves of 64 x 128 (default 8 of 64 x 64), fragments read half a K step ahead (default a
-    whole step), on short and long K slices."""
-    monkeypatch.setenv("TFP8_GEMM_STAGES", stages)
-    monkeypatch.setenv("TFP8_GEMM_WN", wn)
-    monkeypatch.setenv("TFP8_GEMM_RA", ra)
-    _run(130, 520, 128, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=3)
-    _run(256, 768, 3072, None, torch.bfloat16, xdt=torch.bfloat16, seed=4)
+@pytest.mark.parametrize("cfg", list(range(1, 8)))
+def test_direct_gemm_every_config(cfg, monkeypatch):
+    """Every direct-load GEMM configuration (block tile 32/64/128 x 128/256, 4 or 8 waves, rings of
+    3 to 7 K steps), forced through the library's tuning hooks at small and large M: rows past M
+    inside a tile, several row tiles, columns past N, one-step and long K slices."""
+    monkeypatch.setenv("TFP8_GEMM_DIRECT_MIN_M", "9")
+    monkeypatch.setenv("TFP8_GEMM_DCFG", str(cfg))
+    _run(20, 520, 64, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=cfg)
+    _run(100, 392, 1088, None, torch.bfloat16, fmt="e5m2", xdt=torch.bfloat16, seed=cfg + 1)
+    _run(300, 1024, 3072, None, torch.float32, xdt=torch.float16, seed=cfg + 2)
 
 
 @pytest.mark.parametrize("nt,w,d", [(2, 8, 4), (2, 8, 8), (2, 4, 4), (2, 4, 8), (1, 8, 4), (1, 8, 8), (1, 4, 4), (1, 4, 8)])
