@@ -10,7 +10,13 @@ and the FP8Linear path counters.  Layout choices for the GPU:
   * the KV cache is preallocated [B, heads, max_len, head_dim] and written in place;
   * attention runs in fp32 on contiguous operands (scores, causal mask, softmax, values);
   * the tied output head keeps one fp32 copy of the embedding (the reference re-widens the
-    embedding to fp32 on every call, demo_llm.py:127).
+    embedding to fp32 on every call, demo_llm.py:127);
+  * decoding can be replayed from one captured HIP graph (GraphDecoder): the step has static
+    shapes -- the position is a device tensor that drives the rotary angles, the KV-cache write and
+    the attention mask over the whole (zero-filled) cache -- and the greedy token and the position
+    are updated on the device, so a token costs one graph launch instead of ~400 kernel launches
+    from Python.  Prefill (static shape for a given prompt length) is captured the same way for
+    the latency figure.
 """
 import argparse
 import math
@@ -80,6 +86,27 @@ class Attention(nn.Module):
         o = torch.matmul(torch.softmax(scores, -1), vals.contiguous())           # [B, H, T, hd]
         return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
 
+    def forward_static(self, x, cos, sin, cache, pos, kpos):
+        """One decode position with static shapes: x [B, 1, d], pos int64 [1] on the device, kpos =
+        arange(max_len).  The cache row at pos is written with index_copy_ and attention covers the
+        whole cache, positions past pos masked (cache rows past pos must be finite: zero-filled)."""
+        B, T, _ = x.shape
+        q = _rotary(self.q_proj(x).view(B, T, self.nh, self.hd), cos, sin)
+        k = _rotary(self.k_proj(x).view(B, T, self.nkv, self.hd), cos, sin)
+        v = self.v_proj(x).view(B, T, self.nkv, self.hd)
+        kc, vc = cache
+        kc.index_copy_(2, pos, k.transpose(1, 2))
+        vc.index_copy_(2, pos, v.transpose(1, 2))
+        rep = self.nh // self.nkv
+        keys, vals = kc.float(), vc.float()
+        if rep > 1:
+            keys, vals = keys.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
+        qf = q.transpose(1, 2).float().contiguous()                          # [B, H, 1, hd]
+        scores = torch.matmul(qf, keys.transpose(-1, -2).contiguous()) / math.sqrt(self.hd)
+        scores = scores.masked_fill(kpos > pos, float("-inf"))
+        o = torch.matmul(torch.softmax(scores, -1), vals.contiguous())
+        return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
+
 
 class MLP(nn.Module):
     def __init__(self, c):
@@ -104,6 +131,10 @@ class Block(nn.Module):
         x = x + self.self_attn(self.input_layernorm(x), cos, sin, cache, start)
         return x + self.mlp(self.post_attention_layernorm(x))
 
+    def forward_static(self, x, cos, sin, cache, pos, kpos):
+        x = x + self.self_attn.forward_static(self.input_layernorm(x), cos, sin, cache, pos, kpos)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
 
 class Llama(nn.Module):
     def __init__(self, c):
@@ -119,11 +150,12 @@ class Llama(nn.Module):
                 nn.init.normal_(m.weight, std=0.02)
         self._head32 = None
 
-    def new_cache(self, B, max_len):
+    def new_cache(self, B, max_len, zero=False):
         c, p = self.c, self.embed.weight
         hd = c["dim"] // c["n_heads"]
-        return [(torch.empty(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device),
-                 torch.empty(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device)) for _ in self.layers]
+        new = torch.zeros if zero else torch.empty
+        return [(new(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device),
+                 new(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device)) for _ in self.layers]
 
     def _rope(self, start, T, device):
         hd = self.c["dim"] // self.c["n_heads"]
@@ -131,15 +163,116 @@ class Llama(nn.Module):
         ang = torch.arange(start, start + T, device=device, dtype=torch.float32)[:, None] * inv[None, :]
         return ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
 
+    def _head(self, x):
+        if self._head32 is None or self._head32.device != x.device:
+            self._head32 = self.embed.weight.detach().float()
+        return F.linear(self.norm(x).float(), self._head32)
+
     def forward(self, ids, cache, start=0):
         """Logits (fp32) for every position of ids [B, T], appending to cache at `start`."""
         cos, sin = self._rope(start, ids.shape[1], ids.device)
         x = self.embed(ids)
         for layer, kv in zip(self.layers, cache):
             x = layer(x, cos, sin, kv, start)
-        if self._head32 is None or self._head32.device != x.device:
-            self._head32 = self.embed.weight.detach().float()
-        return F.linear(self.norm(x).float(), self._head32)
+        return self._head(x)
+
+    def decode_step(self, tok, cache, pos, kpos):
+        """One greedy decode step with static shapes and device-resident state (capturable in a
+        HIP graph): consumes tok [B, 1] at position pos (int64 [1]), returns the logits [B, 1, V],
+        writes the next greedy token into tok and advances pos.  pos must be below the cache
+        length: it indexes the cache write on the device (GraphDecoder checks it on the host)."""
+        hd = self.c["dim"] // self.c["n_heads"]
+        inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=tok.device, dtype=torch.float32) * 2.0 / hd))
+        ang = pos.float()[:, None] * inv[None, :]
+        cos, sin = ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
+        x = self.embed(tok)
+        for layer, kv in zip(self.layers, cache):
+            x = layer.forward_static(x, cos, sin, kv, pos, kpos)
+        logits = self._head(x)
+        tok.copy_(greedy(logits[:, -1]))
+        pos.add_(1)
+        return logits
+
+
+def greedy(logits):
+    """argmax over the last dim of [B, V] logits as [B, 1], first maximum on ties (as torch.argmax).
+    Two levels of per-row reductions (128-wide chunks, then the chunk maxima), so that no
+    reduction spans thread blocks: such reductions clear a counter with a memset node, which has
+    given wrong results on graph replays after the first."""
+    B, V = logits.shape
+    if V % 128:
+        return logits.argmax(-1, keepdim=True)
+    cmax, cidx = logits.view(B, V // 128, 128).max(-1)                      # per chunk
+    c = cmax.argmax(-1, keepdim=True)                                       # first chunk holding the max
+    return c * 128 + cidx.gather(1, c)
+
+
+class GraphDecoder:
+    """Greedy decoding replayed from one captured HIP graph (torch.cuda.CUDAGraph) per batch size:
+    the graph holds the whole decode step of Llama.decode_step, its KV cache, token and position
+    are static device tensors, and the prompt is prefilled eagerly into the same cache."""
+
+    def __init__(self, model, B, max_len):
+        dev = model.embed.weight.device
+        self.model, self.B, self.max_len = model, B, max_len
+        self.cache = model.new_cache(B, max_len, zero=True)
+        self.tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.kpos = torch.arange(max_len, device=dev)
+        self.graph = self.logits = None
+        self.next_pos = 0          # host mirror of pos: a step writes cache row pos, so pos < max_len
+
+    @torch.no_grad()
+    def capture(self):
+        # Warm-up outside the capture: FP8Linear checks its first outputs on the host, and the
+        # libraries pick their kernels; then the state is cleared.
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):         # positions 0..2, inside the cache (reset below)
+                self.model.decode_step(self.tok, self.cache, self.pos, self.kpos)
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self.model.decode_step(self.tok, self.cache, self.pos, self.kpos)
+        self.reset()
+        return self
+
+    def reset(self):
+        for kc, vc in self.cache:
+            kc.zero_()
+            vc.zero_()
+        self.pos.zero_()
+        self.tok.zero_()
+        self.next_pos = 0
+
+    def rewind(self, pos):
+        """Continue decoding from position pos (cache rows from pos on are overwritten)."""
+        if not 0 <= pos < self.max_len:
+            raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
+        self.pos.fill_(pos)
+        self.next_pos = pos
+
+    @torch.no_grad()
+    def prefill(self, prompt):
+        """Eager prefill of prompt [B, T] into the cache; leaves the first greedy token in tok."""
+        if prompt.shape[1] >= self.max_len:
+            raise ValueError(f"prompt of {prompt.shape[1]} tokens leaves no room in the cache (max_len {self.max_len})")
+        self.reset()
+        logits = self.model(prompt, self.cache, 0)
+        self.tok.copy_(greedy(logits[:, -1]))
+        self.rewind(prompt.shape[1])
+        return logits
+
+    def step(self):
+        """One decode step (one graph launch): returns the step's logits [B, 1, V] (overwritten by
+        the next step) and leaves the next token in self.tok.  Raises once the cache is full: the
+        step writes cache row pos, and the graph cannot check that on the device."""
+        if self.next_pos >= self.max_len:
+            raise RuntimeError(f"KV cache full ({self.max_len} positions)")
+        self.graph.replay()
+        self.next_pos += 1
+        return self.logits
 
 
 def build(size="c5", dtype=torch.bfloat16, device="cuda", seed=0):
@@ -185,10 +318,13 @@ def _median_ms(fn, n):
 
 
 @torch.no_grad()
-def timings(model, B, prompt_len, n_decode, vocab):
+def timings(model, B, prompt_len, n_decode, vocab, graphs=True):
+    """Eager prefill and per-token decode latency (ms); with graphs also the prefill and decode
+    replayed from captured HIP graphs.  Returns (prefill, decode) or (prefill, decode,
+    prefill_graph, decode_graph)."""
     ids = torch.randint(0, vocab, (B, prompt_len), device="cuda")
     cache = model.new_cache(B, prompt_len + n_decode + 8)
-    for _ in range(2):
+    for _ in range(3):
         model(ids, cache, 0)
     prefill = _median_ms(lambda: model(ids, cache, 0), 5)
     tok = ids[:, -1:]
@@ -198,7 +334,22 @@ def timings(model, B, prompt_len, n_decode, vocab):
         for i in range(n_decode):
             model(tok, cache, prompt_len + i)
     per_tok = _median_ms(steps, 3) / n_decode
-    return prefill, per_tok
+    if not graphs:
+        return prefill, per_tok
+    pg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(pg):
+        model(ids, cache, 0)
+    prefill_g = _median_ms(pg.replay, 5)
+    dec = GraphDecoder(model, B, prompt_len + n_decode + 8).capture()
+    dec.prefill(ids)
+
+    def gsteps():                   # every timed run decodes the same n_decode positions
+        dec.rewind(prompt_len)
+        for _ in range(n_decode):
+            dec.step()
+    gsteps()
+    per_tok_g = _median_ms(gsteps, 3) / n_decode
+    return prefill, per_tok, prefill_g, per_tok_g
 
 
 def run(size="c5", prompt_len=512, n_decode=128, batches=(1, 8)):
@@ -211,7 +362,10 @@ def run(size="c5", prompt_len=512, n_decode=128, batches=(1, 8)):
     ids = torch.randint(0, c["vocab"], (1, prompt_len), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
     with torch.no_grad():
         ref = model(ids, model.new_cache(1, prompt_len), 0)
-    base_t = {B: timings(model, B, prompt_len, n_decode, c["vocab"]) for B in batches}
+    base_t = {}
+    for B in batches:
+        print(f"[demo] timing the bf16 model at B={B}", flush=True)
+        base_t[B] = timings(model, B, prompt_len, n_decode, c["vocab"])
     bf16_mb = sum(weight_bytes(model).values()) / 2**20
     prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn", weight_group=None, nan_check=True))
     fp8_mb = sum(weight_bytes(model).values()) / 2**20
@@ -222,10 +376,13 @@ def run(size="c5", prompt_len=512, n_decode=128, batches=(1, 8)):
     print(f"weights+state bf16 {bf16_mb:.1f} MB -> fp8 {fp8_mb:.1f} MB")
     print(f"logits vs bf16: cosine {cos:.6f}  relative L2 {rel:.4f}  top-1 {100 * top1:.2f}%")
     for B in batches:
-        p, d = timings(model, B, prompt_len, n_decode, c["vocab"])
-        pb, db = base_t[B]
+        print(f"[demo] timing the FP8 model at B={B}", flush=True)
+        p, d, pg, dg = timings(model, B, prompt_len, n_decode, c["vocab"])
+        pb, db, pgb, dgb = base_t[B]
         print(f"B={B}: prefill {prompt_len} tok {p:8.2f} ms (bf16 {pb:8.2f})  decode/token {d:7.3f} ms (bf16 {db:7.3f})  "
               f"-> {B * prompt_len / p * 1e3:9.0f} prefill tok/s, {B / d * 1e3:8.0f} decode tok/s")
+        print(f"B={B} HIP graphs: prefill {pg:8.2f} ms (bf16 {pgb:8.2f})  decode/token {dg:7.3f} ms (bf16 {dgb:7.3f})  "
+              f"-> {B * prompt_len / pg * 1e3:9.0f} prefill tok/s, {B / dg * 1e3:8.0f} decode tok/s")
     paths = {}
     for m in model.modules():
         if isinstance(m, FP8Linear):

@@ -139,3 +139,57 @@ def test_c5_prefill_and_greedy_decode():
             stats[k] = stats.get(k, 0) + v
     print(f"[c5] FP8Linear paths {stats}", flush=True)
     assert stats["gemv"] > 0 and stats["gemm"] + stats["chunked"] > 0 and stats["fallback"] == 0
+
+
+def test_graph_decode_replays_match_eager():
+    """GraphDecoder: the decode step captured once as a HIP graph (position and token are device
+    tensors, the cache is static) and replayed.  Every replay, over two passes of the same prompt
+    with host synchronizations and eager work between replays, must give the tokens and logits of
+    the same static-shape step run eagerly; and the static step (attention over the whole
+    zero-filled cache, masked past the position) must decode the tokens of the dynamic-shape
+    forward used everywhere else."""
+    model = demo_llm.build("tiny")
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn"))
+    B, T, NEW = 2, 24, 12
+    prompt = torch.randint(0, model.c["vocab"], (B, T), device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    print(f"[graph] tiny B={B} prompt {T} decode {NEW}", flush=True)
+    with torch.no_grad():
+        toks_dyn, _, steps_dyn = demo_llm.generate(model, prompt, NEW + 1)
+        eager = demo_llm.GraphDecoder(model, B, T + NEW + 4)
+        eager.prefill(prompt)
+        e_toks, e_logits = [], []
+        for _ in range(NEW):
+            e_logits.append(model.decode_step(eager.tok, eager.cache, eager.pos, eager.kpos)[:, -1].clone())
+            e_toks.append(eager.tok.clone())
+    # static step vs dynamic forward: the same tokens; the logits differ only because attention
+    # sums over the longer (masked, zero-filled) cache in another fp32 order, which flips bf16
+    # roundings of the projections downstream (the noise floor of the C5 test above, ~3e-3)
+    assert torch.equal(torch.cat(e_toks, 1), toks_dyn[:, 1:]), "static decode step diverged from the forward"
+    cos, rel, top1 = demo_llm.agreement(steps_dyn[:, 1:], torch.stack(e_logits, 1))
+    print(f"[graph] static step vs forward: cosine {cos:.7f} rel L2 {rel:.2e} top-1 {100 * top1:.1f}%", flush=True)
+    assert rel < 1e-2 and cos > 0.9999 and top1 == 1.0, (cos, rel, top1)
+
+    dec = demo_llm.GraphDecoder(model, B, T + NEW + 4).capture()
+    for rep in range(2):
+        dec.prefill(prompt)
+        tok0 = dec.tok.clone()
+        for i in range(NEW):
+            lg = dec.step()[:, -1].clone()
+            if i % 3 == 0:
+                torch.cuda.synchronize()
+                _ = (lg * 2).sum().item()          # eager work and a host sync between replays
+            assert torch.equal(dec.tok, e_toks[i]), (rep, i)
+            torch.testing.assert_close(lg, e_logits[i], rtol=1e-5, atol=1e-6)
+    print("[graph] every replay matches the eager step", flush=True)
+    # the host refuses a step past the cache (the graph's cache write cannot check its position)
+    assert dec.next_pos == T + NEW
+    for _ in range(dec.max_len - dec.next_pos):
+        dec.step()
+    with pytest.raises(RuntimeError, match="KV cache full"):
+        dec.step()
+    with pytest.raises(ValueError):
+        dec.rewind(dec.max_len)
+    dec.rewind(T)                  # rows below T still hold the prompt; restart from its first token
+    dec.tok.copy_(tok0)
+    dec.step()
+    assert torch.equal(dec.tok, e_toks[0]) and dec.next_pos == T + 1
