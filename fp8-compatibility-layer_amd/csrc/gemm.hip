@@ -547,7 +547,7 @@ int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, cons
     // Decode sizes go to the matrix-core decode kernel (no split-K); then the direct-to-LDS GEMM
     // (one scale per weight row, from its minimum M up), the weight-streaming kernel (M <= 128)
     // and the LDS-tiled kernel below, the general path.
-    if (M <= 8 && M >= gemv_mfma_min_m()) {
+    if (M <= env_int("TFP8_GEMV_MFMA_MAX_M", 8) && M >= gemv_mfma_min_m()) {
         const int rm = run_gemv_mfma(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rm != 1) return rm;
     }
