@@ -19,6 +19,7 @@
 // MFMA; no decoded weight is ever written to LDS or HBM.  The scale, xs and bias are applied in
 // the epilogue, or by the split-K reduction when K is split over gridDim.y.
 #include <algorithm>
+#include <type_traits>
 
 #include "tfp8_common.h"
 
@@ -39,24 +40,39 @@ template <> struct GdOp<_Float16> {
     static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
-    template <int FMT> static __device__ __forceinline__ uint32_t cvt(uint32_t w, bool hi) { return cvt2_f16<FMT>(w, hi); }
+    template <int FMT> static __device__ __forceinline__ uint32_t cvt(uint32_t w, float s, bool hi) {
+        f16x2 v;
+        if constexpr (FMT == TFP8_E4M3FN) v = hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, s, true) : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, s, false);
+        else v = hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, s, true) : __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, s, false);
+        return __builtin_bit_cast(uint32_t, v);
+    }
 };
 template <> struct GdOp<__bf16> {
     typedef bf16x8 V;
     static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
-    template <int FMT> static __device__ __forceinline__ uint32_t cvt(uint32_t w, bool hi) { return cvt2_bf16<FMT>(w, hi); }
+    template <int FMT> static __device__ __forceinline__ uint32_t cvt(uint32_t w, float s, bool hi) {
+        bf16x2 v;
+        if constexpr (FMT == TFP8_E4M3FN) v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, s, true) : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, s, false);
+        else v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, s, true) : __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, s, false);
+        return __builtin_bit_cast(uint32_t, v);
+    }
 };
 
-// 8 codes (two dwords, k order) -> one 16-bit MFMA operand.
+// Scale handling: one scale per weight row (applied after the sum), UE8M0 K groups folded into
+// the decode (the conversion multiplies by the scale's power of two, exact in bf16), or K groups
+// (G % 64 == 0) applied to an fp32 partial sum at every group boundary (exact for any f32 scale).
+enum { GD_CHANNEL = 0, GD_FOLD = 1, GD_PARTIAL = 2 };
+
+// 8 codes (two dwords, k order) times the power of two of s -> one 16-bit MFMA operand.
 template <typename T, int FMT>
-__device__ __forceinline__ typename GdOp<T>::V gd_decode(uint32_t lo, uint32_t hi) {
+__device__ __forceinline__ typename GdOp<T>::V gd_decode(uint32_t lo, uint32_t hi, float s) {
     uint4 u;
-    u.x = GdOp<T>::template cvt<FMT>(lo, false);
-    u.y = GdOp<T>::template cvt<FMT>(lo, true);
-    u.z = GdOp<T>::template cvt<FMT>(hi, false);
-    u.w = GdOp<T>::template cvt<FMT>(hi, true);
+    u.x = GdOp<T>::template cvt<FMT>(lo, s, false);
+    u.y = GdOp<T>::template cvt<FMT>(lo, s, true);
+    u.z = GdOp<T>::template cvt<FMT>(hi, s, false);
+    u.w = GdOp<T>::template cvt<FMT>(hi, s, true);
     return __builtin_bit_cast(typename GdOp<T>::V, u);
 }
 
@@ -89,11 +105,11 @@ __device__ __forceinline__ void gd_wait_vm(int stages) {
 
 // Block tile BM x BN (BM = 32, 64 or 128 activation rows; BN = 128 or 256 weight rows), WM x WN
 // waves, ring of S K steps.
-template <typename T, int FMT, int BM, int BN, int WM, int WN, int S>
+template <typename T, int FMT, int BM, int BN, int WM, int WN, int S, int SMODE>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     const T* __restrict__ x, const float* __restrict__ xs, const uint8_t* __restrict__ w,
     const void* __restrict__ ws, int sk, const float* __restrict__ bias, void* __restrict__ y, int ydt,
-    int M, int N, int K, float* __restrict__ part, int slice_len) {
+    int M, int N, int K, int G, float* __restrict__ part, int slice_len) {
     using Op = GdOp<T>;
     typedef typename Op::V V;
     constexpr int NW = WM * WN;
@@ -126,6 +142,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         (void*)(x + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * (uint32_t)K * 2u), (int)GD_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(w + (size_t)n0 * K), (short)0, (int)((uint32_t)min(BN, N - n0) * (uint32_t)K), (int)GD_BUF_FLAGS);
+
+    // K-group scales of the block's rows for the groups its K slice touches, staged in LDS once
+    // (UE8M0 bytes for folding, f32 values for the partial sums) before any ring load is issued.
+    extern __shared__ __attribute__((aligned(16))) uint8_t gd_scales[];
+    const int gfirst = SMODE == GD_CHANNEL ? 0 : kbeg / G;
+    const int nsg = SMODE == GD_CHANNEL ? 0 : (kbeg + nst * GD_BK - 1) / G - gfirst + 1;
+    if constexpr (SMODE != GD_CHANNEL) {
+        const int ng = K / G;
+        for (int i = tid; i < BN * nsg; i += NW * 64) {
+            const int r = i / nsg, n = min(n0 + r, N - 1);
+            const size_t src = (size_t)n * ng + gfirst + (i - r * nsg);
+            if constexpr (SMODE == GD_FOLD) gd_scales[i] = ((const uint8_t*)ws)[src];
+            else ((float*)gd_scales)[i] = sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[src])
+                                                                : ((const float*)ws)[src];
+        }
+        __syncthreads();
+    }
 
     // LDS layouts (16-byte units): activation row r (128 B) keeps chunk c at c ^ ((r >> 1) & 7),
     // weight row r (64 B) keeps chunk c at c ^ ((r >> 2) & 3); both make the 16-row fragment
@@ -166,17 +199,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         b_rd[p] = ABYTES + (uint32_t)(wn * WTN + l32) * 64u + 16u * (uint32_t)((2 * p + h) ^ bswz);
     }
 
-    f32x16 acc[TM][TN];
+    constexpr bool PART = SMODE == GD_PARTIAL;
+    f32x16 acc[TM][TN], prt[PART ? TM : 1][PART ? TN : 1];
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
+    if constexpr (PART) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) prt[a][b][i] = 0.f;
+    }
+    // This lane's column of tile tn inside the block, and its row of the staged scales.
+    auto scale_row = [&](int tn) { return (wn * WTN + tn * 32 + l32) * nsg; };
 
     struct Frag {
         V a[TM][2];
         uint4 b[TN];
+        float s[SMODE == GD_FOLD ? TN : 1];   // folded UE8M0 scale of the window's group, per tile
     };
     auto read = [&](int st, int p, Frag& f) {
         const uint8_t* base = smem + (st % S) * STAGE;
@@ -186,16 +231,46 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int q = 0; q < 2; ++q) f.a[tm][q] = *(const V*)(base + a_rd[p][q] + tm * 4096);
+        if constexpr (SMODE == GD_FOLD) {
+            // G % 32 == 0: the window's 32 codes (both lane halves) lie in one group
+            const int g = (kbeg + st * GD_BK + 32 * p) / G - gfirst;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) f.s[tn] = ue8m0_to_f32(gd_scales[scale_row(tn) + g]);
+        }
     };
     auto mma = [&](const Frag& f) {
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                const V bq = q ? gd_decode<T, FMT>(f.b[tn].z, f.b[tn].w) : gd_decode<T, FMT>(f.b[tn].x, f.b[tn].y);
+                const float sc = SMODE == GD_FOLD ? f.s[SMODE == GD_FOLD ? tn : 0] : 1.f;
+                const V bq = q ? gd_decode<T, FMT>(f.b[tn].z, f.b[tn].w, sc) : gd_decode<T, FMT>(f.b[tn].x, f.b[tn].y, sc);
 #pragma unroll
-                for (int tm = 0; tm < TM; ++tm) acc[tm][tn] = Op::mma(f.a[tm][q], bq, acc[tm][tn]);
+                for (int tm = 0; tm < TM; ++tm) {
+                    if constexpr (PART) prt[tm][tn] = Op::mma(f.a[tm][q], bq, prt[tm][tn]);
+                    else acc[tm][tn] = Op::mma(f.a[tm][q], bq, acc[tm][tn]);
+                }
             }
+    };
+    // Partial sums: after the last K step of a group (G % 64 == 0) or of the slice, acc += prt * s.
+    auto fold_group = [&](int t) {
+        if constexpr (PART) {
+            const int kn = kbeg + (t + 1) * GD_BK;
+            if (kn % G == 0 || t == nst - 1) {
+                const int g = (kn - 1) / G - gfirst;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    const float sc = ((const float*)gd_scales)[scale_row(tn) + g];
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            acc[tm][tn][i] = fmaf(prt[tm][tn][i], sc, acc[tm][tn][i]);
+                            prt[tm][tn][i] = 0.f;
+                        }
+                }
+            }
+        }
     };
     // Stage st is complete in LDS for every wave once each wave has waited for its own loads of it
     // (stages up to `last` have been issued; loads complete in order) and all have passed the barrier.
@@ -223,6 +298,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         mma(c0);
         if (more) read(t + 1, 1, n1);
         mma(c1);
+        fold_group(t);
     };
     int t = 0;
     for (; t + 1 < nst; t += 2) {
@@ -248,8 +324,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
                     if (row < M) pp[(size_t)row * N + col] = acc[tm][tn][i];
                 }
         } else {
-            const float cs = sk == TFP8_SCALE_UE8M0 ? load_scale<TFP8_SCALE_UE8M0>(ws, (size_t)col)
-                                                    : load_scale<TFP8_SCALE_F32>(ws, (size_t)col);
+            const float cs = SMODE != GD_CHANNEL          ? 1.f
+                             : sk == TFP8_SCALE_UE8M0 ? load_scale<TFP8_SCALE_UE8M0>(ws, (size_t)col)
+                                                      : load_scale<TFP8_SCALE_F32>(ws, (size_t)col);
             const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
@@ -305,10 +382,18 @@ GdCfg gd_cfg(int M) {
 
 }  // namespace
 
-// Whether this kernel takes the shape, and its split of K (slices of whole 64-wide steps until
-// the grid has a block per CU, slices of at least 1024).
-bool gemm_direct_plan(int M, int N, int K, int G, int* slices, int* slice_len) {
-    if (G != K || K % GD_BK != 0 || M < gd_min_m() || !gd_env_int("TFP8_GEMM_DIRECT", 1)) return false;
+// Scale mode for (G, scale kind, activation dtype), or -1 where this kernel does not apply.
+static int gd_mode(int K, int G, int ws_kind, int x16_dtype) {
+    if (G == K) return GD_CHANNEL;
+    if (ws_kind == TFP8_SCALE_UE8M0 && x16_dtype == TFP8_BF16 && G % 32 == 0) return GD_FOLD;
+    if (G % 64 == 0) return GD_PARTIAL;
+    return -1;
+}
+
+// Split of K: slices of whole 64-wide steps until the grid has a block per CU, slices of at least
+// 1024.  Depends on the shape only (the workspace is sized from it).
+static bool gd_split(int M, int N, int K, int* slices, int* slice_len) {
+    if (K % GD_BK != 0 || M < gd_min_m() || !gd_env_int("TFP8_GEMM_DIRECT", 1)) return false;
     const GdCfg c = gd_cfg(M);
     if ((long)c.bn * K >= (1L << 31) || (long)c.bm * K * 2 >= (1L << 31)) return false;
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
@@ -323,35 +408,72 @@ bool gemm_direct_plan(int M, int N, int K, int G, int* slices, int* slice_len) {
     return true;
 }
 
+// Whether this kernel takes the GEMM, with its split of K, scale mode and dynamic LDS (the staged
+// K-group scales of a block: they and the ring must fit the 160 KB of a workgroup; K-group modes
+// exist for the default tiles only).
+static bool gd_plan(int M, int N, int K, int G, int ws_kind, int x16_dtype, int* slices, int* slice_len, int* mode,
+                    size_t* dyn) {
+    const int md = gd_mode(K, G, ws_kind, x16_dtype);
+    if (md < 0 || !gd_split(M, N, K, slices, slice_len)) return false;
+    const GdCfg c = gd_cfg(M);
+    *mode = md;
+    *dyn = 0;
+    if (md != GD_CHANNEL) {
+        const bool dflt = (c.bm == 128 && c.bn == 256 && c.wm == 2 && c.wn == 4 && c.stages == 4) ||
+                          (c.bm == 128 && c.bn == 128 && c.wm == 2 && c.wn == 4 && c.stages == 6);
+        if (!dflt) return false;
+        const size_t groups = (size_t)(*slice_len / G + 2);   // groups one slice can touch
+        *dyn = (c.bn * groups * (md == GD_FOLD ? 1 : 4) + 15) / 16 * 16;
+    }
+    const size_t ring = (size_t)c.stages * (c.bm * GD_BK * 2 + c.bn * GD_BK);
+    return ring + *dyn <= (size_t)GD_LDS_MAX;
+}
+
 size_t gemm_direct_partial_bytes(int M, int N, int K) {
     int s, len;
-    if (!gemm_direct_plan(M, N, K, K, &s, &len)) return 0;
+    if (!gd_split(M, N, K, &s, &len)) return 0;
     return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
                           const float* bias, void* y, int ydt, hipStream_t s);
 
-template <typename T, int FMT>
-static void gd_launch(int slices, int slice_len, const void* x, const float* xs, const uint8_t* w, const void* ws,
-                      int sk, const float* bias, void* y, int ydt, int M, int N, int K, float* part, hipStream_t s) {
+template <typename T, int FMT, int SMODE>
+static void gd_launch(int slices, int slice_len, size_t dyn, const void* x, const float* xs, const uint8_t* w,
+                      const void* ws, int sk, const float* bias, void* y, int ydt, int M, int N, int K, int G,
+                      float* part, hipStream_t s) {
     const GdCfg c = gd_cfg(M);
     const dim3 grid(((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn), slices);
 #define GD_K(BM_, BN_, WM_, WN_, S_)                                                                           \
     if (c.bm == BM_ && c.bn == BN_ && c.wm == WM_ && c.wn == WN_ && c.stages == S_) {                          \
-        gemm_direct_kernel<T, FMT, BM_, BN_, WM_, WN_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(                    \
-            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, part, slice_len);                               \
+        gemm_direct_kernel<T, FMT, BM_, BN_, WM_, WN_, S_, SMODE><<<grid, 64 * WM_ * WN_, dyn, s>>>(           \
+            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, part, slice_len);                            \
         return;                                                                                                \
     }
     GD_K(128, 256, 2, 4, 4)
-    GD_K(128, 256, 2, 2, 4)
-    GD_K(128, 256, 2, 4, 3)
-    GD_K(128, 256, 2, 4, 5)
-    GD_K(64, 256, 2, 4, 6)
-    GD_K(32, 256, 1, 4, 7)
     GD_K(128, 128, 2, 4, 6)
-    GD_K(64, 128, 2, 2, 7)
+    if constexpr (SMODE == GD_CHANNEL) {
+        GD_K(128, 256, 2, 2, 4)
+        GD_K(128, 256, 2, 4, 3)
+        GD_K(128, 256, 2, 4, 5)
+        GD_K(64, 256, 2, 4, 6)
+        GD_K(32, 256, 1, 4, 7)
+        GD_K(64, 128, 2, 2, 7)
+    }
 #undef GD_K
+}
+
+template <typename T, int FMT>
+static void gd_launch_mode(int mode, int slices, int slice_len, size_t dyn, const void* x, const float* xs,
+                           const uint8_t* w, const void* ws, int sk, const float* bias, void* y, int ydt, int M, int N,
+                           int K, int G, float* part, hipStream_t s) {
+    if (mode == GD_PARTIAL)
+        gd_launch<T, FMT, GD_PARTIAL>(slices, slice_len, dyn, x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, part, s);
+    else if (mode == GD_FOLD) {
+        if constexpr (std::is_same<T, __bf16>::value)
+            gd_launch<T, FMT, GD_FOLD>(slices, slice_len, dyn, x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, part, s);
+    } else
+        gd_launch<T, FMT, GD_CHANNEL>(slices, slice_len, dyn, x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, part, s);
 }
 
 // Runs this GEMM if it takes the shape; returns 1 if it did not (caller falls back), 0 or an
@@ -360,19 +482,20 @@ static void gd_launch(int slices, int slice_len, const void* x, const float* xs,
 int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
                     const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
                     float* partial, hipStream_t s) {
-    int slices, slice_len;
-    if (!gemm_direct_plan(M, N, K, G, &slices, &slice_len)) return 1;
+    int slices, slice_len, mode;
+    size_t dyn;
+    if (!gd_plan(M, N, K, G, ws_kind, x16_dtype, &slices, &slice_len, &mode, &dyn)) return 1;
     float* part = slices > 1 ? partial : nullptr;
     if (x16_dtype == TFP8_BF16) {
-        TFP8_DISPATCH_FMT(fmt, F, gd_launch<__bf16, F>(slices, slice_len, x16, xs, w, ws, ws_kind, bias, y, y_dtype, M,
-                                                       N, K, part, s));
+        TFP8_DISPATCH_FMT(fmt, F, gd_launch_mode<__bf16, F>(mode, slices, slice_len, dyn, x16, xs, w, ws, ws_kind,
+                                                            bias, y, y_dtype, M, N, K, G, part, s));
     } else {
-        TFP8_DISPATCH_FMT(fmt, F, gd_launch<_Float16, F>(slices, slice_len, x16, xs, w, ws, ws_kind, bias, y, y_dtype,
-                                                         M, N, K, part, s));
+        TFP8_DISPATCH_FMT(fmt, F, gd_launch_mode<_Float16, F>(mode, slices, slice_len, dyn, x16, xs, w, ws, ws_kind,
+                                                              bias, y, y_dtype, M, N, K, G, part, s));
     }
     int rc = check_launch("tfp8_gemm (direct)");
     if (rc || slices <= 1) return rc;
-    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, 1, xs, bias, y, y_dtype, s);
+    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, mode == GD_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, s);
     return check_launch("tfp8_gemm (direct) splitk reduce");
 }
 

@@ -355,6 +355,23 @@ def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, monkeypatch
     _run(M, N, K, None, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=M + K)
 
 
+@pytest.mark.parametrize("M,N,K,G,sf,xdt,fmt,split", [
+    (100, 520, 1088, 32, "ue8m0", torch.bfloat16, "e5m2", 0),      # UE8M0 folded into the decode, 128 x 128 tiles
+    (256, 4096, 11008, 32, "ue8m0", torch.bfloat16, "e5m2", 0),    # C4's weights at M=256 (split 8, ragged last slice)
+    (200, 392, 2048, 64, "f32", torch.float16, "e4m3fn", 0),       # f32 groups: fp32 partial per group
+    (300, 1024, 3072, 128, "ue8m0", torch.float16, "e4m3fn", 0),   # UE8M0 groups with f16 x: partial sums
+    (130, 256, 4096, 128, "f32", torch.bfloat16, "e4m3fn", 0),     # split 8, slices of 4 groups
+    (150, 640, 2304, 192, "f32", torch.bfloat16, "e5m2", 5),       # slices of 512 cut groups of 192
+])
+def test_direct_gemm_group_scales(M, N, K, G, sf, xdt, fmt, split, monkeypatch):
+    """K-group scales on the direct-load GEMM: UE8M0 groups folded into the decode (bf16
+    activations), and f32 / UE8M0 groups with G % 64 == 0 applied to an fp32 partial sum at each
+    group boundary, including split-K slices that start inside a group."""
+    if split:
+        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+    _run(M, N, K, G, torch.float32, fmt=fmt, xdt=xdt, sf=sf, seed=M + G)
+
+
 @pytest.mark.parametrize("cfg", list(range(1, 8)))
 def test_direct_gemm_every_config(cfg, monkeypatch):
     """Every direct-load GEMM configuration (block tile 32/64/128 x 128/256, 4 or 8 waves, rings of
