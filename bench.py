@@ -52,6 +52,11 @@ def c3_bytes(M):
     return N * K + N * 1 + N * 4 + M * K * 2 + M * N * 2
 
 
+# C4: M=128, K=11008, N=4096, E5M2 codes, UE8M0 scales per 32-group, bf16 x and y, no bias.
+C4_M, C4_N, C4_K = 128, 4096, 11008
+C4_BYTES = C4_N * C4_K + C4_N * (C4_K // 32) + C4_M * C4_K * 2 + C4_M * C4_N * 2   # 50,364,416
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -98,6 +103,11 @@ def make_layers(cfg, M, device):
         w = torch.randn(N, K, generator=g, device=device) * 0.02
         w = torch.where(torch.rand(N, K, generator=g, device=device) < 1e-3, w * 20, w)
         bias = None
+    elif cfg == "c4":
+        N, K, G, fmt, sf, pow2, xdt, ydt = C4_N, C4_K, 32, "e5m2", "ue8m0", True, torch.bfloat16, torch.bfloat16
+        g.manual_seed(404)
+        w = torch.distributions.Laplace(0.0, 0.02).sample((N, K)).to(device)
+        bias = None
     else:
         N, K, G, fmt, sf, pow2, xdt, ydt = 8192, 8192, None, "e4m3fn", "ue8m0", True, torch.float16, torch.float16
         g.manual_seed(303)
@@ -105,7 +115,10 @@ def make_layers(cfg, M, device):
         bias = torch.randn(N, generator=g, device=device) * 0.1
     q, s, GG = quantize_weight(w, fmt, G, pow2, sf)
     del w
-    x = torch.randn(M, K, generator=g, device=device).to(xdt)
+    x = torch.randn(M, K, generator=g, device=device)
+    if cfg == "c4":   # rows scaled by 2^u, u in -20..20: a bf16 -> f16 cast would over/underflow
+        x = x * torch.exp2(torch.randint(-20, 21, (M, 1), generator=g, device=device).float())
+    x = x.to(xdt)
     per = q.numel() + s.numel() * s.element_size()
     copies = max(2, -(-ROTATE_BYTES // per) + 1)
     wsb = lib.tfp8_linear_workspace_size(_ext.DTYPE_ID[xdt], M, N, K)
@@ -328,6 +341,13 @@ def main():
             del lm
         out["gemm_sweep"] = gsweep
         del layers
+        log("[bench] C4 M=128 GEMM (E5M2, UE8M0 32-groups): building rotating weights")
+        l4, _, meta4 = make_layers("c4", C4_M, dev)
+        m4 = sorted(time_layers(l4, steps, 5) for _ in range(3))[1]
+        out["c4"] = {"us": round(m4 * 1e6, 2), "gbs": round(C4_BYTES / m4 / 1e9, 1),
+                     "tflops": round(2.0 * C4_M * C4_N * C4_K / m4 / 1e12, 1), "timing": "median of 3 runs"}
+        log(f"[bench] C4 M=128: {out['c4']}")
+        del l4
 
     # ---------------------------------------------------------------- W8A8 block-32 GEMM
     if a.only in (None, "w8a8"):
@@ -371,6 +391,8 @@ def main():
                                                     "UE8M0, f32 bias, fp16 out", **gm["meta"]}}
         if out.get("gemm_sweep"):
             line["gemm_sweep"] = out["gemm_sweep"]
+        if out.get("c4"):
+            line["c4_gemm"] = out["c4"]
     if "w8a8" in out:
         line["w8a8"] = out["w8a8"]
     line["cpu_baseline"] = out.get("cpu")
