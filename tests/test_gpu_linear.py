@@ -437,3 +437,30 @@ def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     _check(outs[1], x, q, s, GG, "e4m3fn", b, torch.bfloat16, "gemv", "decode transposed loads")
+
+
+def test_weight_matrix_past_2gib():
+    """A weight matrix of more than 2^31 bytes (K=16384, N=132096: 2.16 GB of codes): buffer offsets
+    inside every kernel are 32-bit, so the GEMV splits the launch by rows and the GEMMs address the
+    weights per block.  M=1 (GEMV), M=4 (matrix-core decode), M=16 (the weight-streaming kernel
+    declines, the LDS-tiled kernel runs) and M=128 (direct-load GEMM); output columns at both ends
+    of the matrix against the float64 oracle on those rows."""
+    K, N = 16384, 132096
+    assert N * K > 2 ** 31
+    print(f"[linear] N={N} K={K}: {N * K / 2 ** 30:.2f} GiB of codes", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    w = torch.randn(N, K, generator=g, device="cuda") * 0.02
+    q, s, G = quantize_weight(w, "e4m3fn", None, True, "f32")
+    del w
+    torch.cuda.empty_cache()
+    cols = np.r_[0:48, N - 80:N]
+    qs, ss = q[cols].cpu().numpy(), s[cols].cpu().numpy()
+    for M in (1, 4, 16, 128):
+        x = (torch.randn(M, K, generator=g, device="cuda") * 0.5).bfloat16()
+        y = _ext.w8a16(x, q, None, s, None, torch.float32, G, "e4m3fn")
+        ref = O.linear_ref64(_x_eff(x, "gemv" if M <= _ext.GEMV_MAXM else "gemm"), qs, ss, G, "e4m3fn", None)
+        got = y[:, cols].double().cpu().numpy()
+        d = np.abs(got - ref)
+        assert (d <= O.tolerance(ref, "float32")).all(), (M, float(d.max()))
+    del q, s
+    torch.cuda.empty_cache()
