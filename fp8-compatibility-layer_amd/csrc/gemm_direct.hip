@@ -436,7 +436,8 @@ size_t gemm_direct_partial_bytes(int M, int N, int K) {
 }
 
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
-                          const float* bias, void* y, int ydt, hipStream_t s);
+                          const float* bias, void* y, int ydt, int xcw, hipStream_t s);
+int gemm_xcd_cols(int ntm, int ntn, int bn);
 
 template <typename T, int FMT, int SMODE>
 static void gd_launch(int slices, int slice_len, size_t dyn, const void* x, const float* xs, const uint8_t* w,
@@ -495,7 +496,10 @@ int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int 
     }
     int rc = check_launch("tfp8_gemm (direct)");
     if (rc || slices <= 1) return rc;
-    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, mode == GD_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, s);
+    const GdCfg c = gd_cfg(M);
+    const int ntm = (M + c.bm - 1) / c.bm, ntn = (N + c.bn - 1) / c.bn;
+    const int xcw = (ntm * ntn) % 8 == 0 ? gemm_xcd_cols(ntm, ntn, c.bn) : 0;
+    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, mode == GD_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, xcw, s);
     return check_launch("tfp8_gemm (direct) splitk reduce");
 }
 

@@ -80,7 +80,12 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = blockIdx.x * (64 * NW) + wave * (16 * NW);   // this wave's first row
+    // With a multiple of 8 blocks across N, block b covers row block (b & 7) * (nblk / 8) + (b >> 3):
+    // blocks go round-robin over the 8 XCDs, so XCD x then writes one contiguous range of output
+    // columns, which the split-K reduction reads back on the same XCD.
+    const int nblk = gridDim.x;
+    const int bx = (nblk & 7) == 0 ? (int)(blockIdx.x & 7) * (nblk >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    const int nb = bx * (64 * NW) + wave * (16 * NW);   // this wave's first row
     const int kbeg = blockIdx.y * slice_len;
     const int kend = min(K, kbeg + slice_len);
     const int nchunks = (kend - kbeg + KC - 1) / KC;
@@ -375,7 +380,7 @@ static bool gs_dispatch(int tm, int nw, int kcs, int slices, int slice_len, cons
 }
 
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
-                          const float* bias, void* y, int ydt, hipStream_t s);
+                          const float* bias, void* y, int ydt, int xcw, hipStream_t s);
 
 // Runs the streaming GEMM if it takes this shape; returns 1 if it did not (caller falls back),
 // 0 or an error code otherwise. x16 is f16/bf16 [M,K]; the matrix must be below 2^31 bytes.
@@ -405,7 +410,9 @@ int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int 
     if (!ok) return 1;
     int rc = check_launch("tfp8_gemm (stream)");
     if (rc || slices <= 1) return rc;
-    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, gm == GM_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, s);
+    const int nblk = (N + 64 * nw - 1) / (64 * nw);
+    const int xcw = nblk % 8 == 0 ? nblk / 8 * 64 * nw : 0;
+    splitk_reduce_launch(part, slices, M, N, ws, ws_kind, gm == GM_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, xcw, s);
     return check_launch("tfp8_gemm (stream) splitk reduce");
 }
 
