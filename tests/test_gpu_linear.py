@@ -209,15 +209,37 @@ def test_nan_fallback():
 
 
 def test_chunked_backend_counts_and_matches():
-    print("[large-M branch]", flush=True)
-    torch.manual_seed(7)
-    lin = nn.Linear(1024, 330, device="cuda")
-    f = FP8Linear.from_linear(lin, large_m_backend="chunked")
-    f.out_dtype = torch.float16
-    x = torch.randn(300, 1024, device="cuda", dtype=torch.bfloat16)
-    y = f(x)
-    assert f.stats["chunked"] == 1
-    _check(y, x, f.qweight, f.weight_scale, 1024, "e4m3fn", f.bias_f32, torch.float16, "gemm", "chunked")
+    """The large-M (chunked) branch, as the reference's test_chunked_formats_dtypes_and_slices
+    (tests/test_tfp8.py:138-162): both formats, every output dtype, per-channel and 128-groups,
+    with and without bias; then odd / ragged N with workspace_mb=0 (the reference's multi-slice
+    case) against the f16-prepared activations the reference multiplies."""
+    for fmt in ("e4m3fn", "e5m2"):
+        for od in (torch.float16, torch.bfloat16, torch.float32):
+            for G in (None, 128):
+                print(f"[large-M branch] fmt={fmt} out={od} G={G}", flush=True)
+                q, s, GG, b = _layer(192, 512, G, fmt, seed=len(fmt) + (G or 0), bias=G is None)
+                f = FP8Linear(512, 192, bias=G is None, fmt=fmt, group_size=GG, out_dtype=od,
+                              large_m_backend="chunked", device="cuda")
+                f.qweight.copy_(q)
+                f.weight_scale = s
+                if b is not None:
+                    f.bias_f32.copy_(b)
+                x = torch.randn(260, 512, generator=torch.Generator().manual_seed(3)).bfloat16().cuda()
+                y = f(x)
+                assert y.dtype == od and f.stats["chunked"] == 1
+                _check(y, x, q, s, GG, fmt, b, od, "gemm", f"chunked {fmt} {od} G={G}")
+    for N, bias in ((200, True), (330, False), (77, True)):
+        print(f"[large-M branch] N={N} bias={bias} workspace_mb=0", flush=True)
+        torch.manual_seed(N)
+        lin = nn.Linear(1024, N, bias=bias, device="cuda")
+        f = FP8Linear.from_linear(lin, large_m_backend="chunked")
+        f.out_dtype = torch.float16
+        f.workspace_mb = 0
+        x = torch.randn(300, 1024, device="cuda", dtype=torch.bfloat16)
+        y = f(x)
+        assert f.stats["chunked"] == 1
+        _check(y, x, f.qweight, f.weight_scale, f.group_size, "e4m3fn", f.bias_f32, torch.float16, "gemm",
+               f"chunked N={N}")
 
 
 # ------------------------------------------------------------------ BASELINE configs, full size

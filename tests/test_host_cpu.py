@@ -212,6 +212,38 @@ def test_library_exports_every_header_symbol():
     assert _ext.library().tfp8_abi_version() == _ext.ABI_VERSION
 
 
+def _header_prototypes():
+    """{name: (return type, [parameter types])} from the C declarations in the header."""
+    text = re.sub(r"//[^\n]*", "", open(HEADER).read())
+    protos = {}
+    for m in re.finditer(r"^([A-Za-z_][\w\s\*]*?)\b(tfp8_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
+        params = [p.strip() for p in " ".join(m.group(3).split()).split(",")]
+        params = [] if params == ["void"] else params
+        # a parameter's type is everything but its name
+        protos[m.group(2)] = (m.group(1).strip(), [re.sub(r"\s*\b\w+$", "", p).strip() for p in params])
+    return protos
+
+
+def _ctypes_kind(ctype):
+    if "*" in ctype:
+        return ctypes.c_char_p if ctype.replace(" ", "") == "constchar*" else ctypes.c_void_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
+            "float": ctypes.c_float}[ctype]
+
+
+def test_bound_argument_kinds_match_header():
+    """Every entry point is bound with exactly the argument kinds (pointer / int / int64 / size_t)
+    and return kind its C declaration has, in order, so no call can pass an int where a pointer or
+    a 64-bit size is expected (the bug class of the reference's launch-slot test,
+    tests/test_tfp8.py:322-360, at this boundary)."""
+    protos = _header_prototypes()
+    assert sorted(protos) == _header_functions()
+    for name, (ret, params) in protos.items():
+        res, args = _ext._SIGS[name]
+        assert args == [_ctypes_kind(t) for t in params], (name, params)
+        assert res == _ctypes_kind(ret), (name, ret)
+
+
 def test_abi_argument_validation_without_gpu():
     lib = _ext.library()
     assert lib.tfp8_decode(None, -1, 0, None, 0, None) == -1
