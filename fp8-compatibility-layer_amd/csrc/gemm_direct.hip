@@ -85,7 +85,14 @@ __device__ __forceinline__ typename GdOp<T>::V gd_decode(uint32_t lo, uint32_t h
 __device__ __forceinline__ void gd_load_lds(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
                  "s"(soff)
-                 : "memory");
+                 : "memory", "m0");
+}
+
+// Waits until at most N of this wave's load instructions are outstanding.
+template <int N>
+__device__ __forceinline__ void gd_wait_vm_const() {
+    static_assert(N >= 0 && N <= 63, "vmcnt holds at most 63");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // Waits until at most `stages` stages of this wave's loads (L load instructions each) are
@@ -300,7 +307,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         mma(c1);
         fold_group(t);
     };
+    // Steady state, t + S - 1 < nst: every step issues a stage and reads the next fragments, so the
+    // body has no branches and the wait counts are constants.  (With the conditional form above in
+    // the loop, the compiler's wait counts at the merge points had to cover the LDS reads just
+    // issued for the next step: lgkmcnt(0) before the last MFMAs of every step.)  The scheduling
+    // barriers keep each window's reads ahead of the multiplies that overlap them.
+    auto step_full = [&](int t, Frag& c0, Frag& c1, Frag& n0, Frag& n1) {
+        gd_wait_vm_const<(LA + LB) * (S - 3)>();     // stage t + 1 done; t + 2 .. t + S - 2 may be in flight
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(t + S - 1);
+        read(t + 1, 0, n0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(c0);
+        read(t + 1, 1, n1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(c1);
+        fold_group(t);
+    };
     int t = 0;
+    for (; t + 1 < nst - (S - 1); t += 2) {
+        step_full(t, f0, f1, g0, g1);
+        step_full(t + 1, g0, g1, f0, f1);
+    }
     for (; t + 1 < nst; t += 2) {
         step(t, f0, f1, g0, g1);
         step(t + 1, g0, g1, f0, f1);
