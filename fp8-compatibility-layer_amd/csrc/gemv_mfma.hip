@@ -191,7 +191,18 @@ __global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__
         }
     };
 
-    for (int i = 0; i < nch; i += D) {
+    // Steady state (every chunk of the round computed, every chunk D later issued): no branches, so
+    // the compiler's wait counts stay exact.  With the conditional form below in the loop, the merge
+    // points made it wait for every load in flight, D chunks of prefetch notwithstanding.
+    int i = 0;
+    for (; i + 2 * D <= nch; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            compute(d, c0 + i + d);
+            issue(d, c0 + i + d + D);
+        }
+    }
+    for (; i < nch; i += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (i + d < nch) compute(d, c0 + i + d);
