@@ -566,10 +566,11 @@ static int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } retu
 int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
              const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, float* partial,
              hipStream_t s) {
-    // Decode sizes go to the matrix-core decode kernel (no split-K); then the direct-to-LDS GEMM
-    // (one scale per weight row, from its minimum M up), the weight-streaming kernel (M <= 128)
-    // and the LDS-tiled kernel below, the general path.
-    if (M <= env_int("TFP8_GEMV_MFMA_MAX_M", 8) && M >= gemv_mfma_min_m()) {
+    // Up to 16 rows go to the matrix-core decode kernel (no split-K; on MI355X it beats the
+    // weight-streaming kernel at every M from 9 to 16: C3 M=16 15.7 vs 16.9 us, C2 M=16 16.7 vs
+    // 20.7 us); then the direct-to-LDS GEMM (one scale per weight row, from its minimum M up), the
+    // weight-streaming kernel (M <= 128) and the LDS-tiled kernel below, the general path.
+    if (M <= env_int("TFP8_GEMV_MFMA_MAX_M", 16) && M >= gemv_mfma_min_m()) {
         const int rm = run_gemv_mfma(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rm != 1) return rm;
     }

@@ -8,6 +8,8 @@ dtypes, pipeline edges, folded group scales, empty / non-contiguous / N-d input,
 launch state, NaN fallback) and every BASELINE config at its full size, plus the reference's
 CPU dequantize-then-matmul path as a second reference.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -408,7 +410,7 @@ def test_direct_gemm_every_config(cfg, monkeypatch):
 
 @pytest.mark.parametrize("nt,w,d", [(2, 8, 4), (2, 8, 8), (2, 4, 4), (2, 4, 8), (1, 8, 4), (1, 8, 8), (1, 4, 4), (1, 4, 8)])
 def test_decode_mfma_every_config(nt, w, d, monkeypatch):
-    """The matrix-core decode kernel (M <= 8 rows) in every compiled configuration, forced down to
+    """The matrix-core decode kernel (up to 16 rows) in every compiled configuration, forced down to
     M = 1: rows past N in the last block, a K tail that is not a whole 64-byte chunk, K ranges that
     leave some waves without work, per-channel / f32 K-group (G=64) / UE8M0 K-group (G=32) scales,
     both formats, f16 and bf16 activations, with and without bias."""
@@ -423,6 +425,9 @@ def test_decode_mfma_every_config(nt, w, d, monkeypatch):
     # K a multiple of 256 x W: the transposed weight-load layout (rows past N in the last block)
     _run(6, 72, 256 * w * 2, 128, torch.bfloat16, xdt=torch.bfloat16, seed=w * d)
     _run(4, 40, 256 * w, None, torch.float16, fmt="e5m2", xdt=torch.float16, sf="ue8m0", seed=nt)
+    # 9..16 rows (the GEMM entry): bf16 activations, and fp32 ones prepared to f16 with row scales
+    _run(16, 136, 256 * w * 2, 64, torch.bfloat16, xdt=torch.bfloat16, seed=nt + 16)
+    _run(11, 200, 1152, None, torch.float32, xdt=torch.float32, seed=d + 11)
 
 
 @pytest.mark.parametrize("M,N,K,G,sf", [(16, 8192, 8192, None, "ue8m0"), (24, 1000, 2048, 128, "f32"),
@@ -432,6 +437,7 @@ def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
     regrouped through LDS) against its direct operand-layout loads: bit-identical outputs (same
     operands, same order), including the K tail, rows past N and split-K."""
     print(f"[linear] stream transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
+    monkeypatch.setenv("TFP8_GEMV_MFMA_MAX_M", "8")   # M <= 16 would take the matrix-core decode kernel
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().cuda()
     outs = []
@@ -444,7 +450,8 @@ def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
 
 
 @pytest.mark.parametrize("M,N,K,G,sf", [(4, 14336, 4096, 128, "f32"), (8, 4096, 4096, None, "ue8m0"),
-                                        (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32")])
+                                        (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32"),
+                                        (16, 8192, 8192, None, "ue8m0"), (12, 14336, 4096, 128, "f32")])
 def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
     """The decode kernel's transposed weight loads (4 rows x 256 bytes per load, regrouped through
     LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
@@ -458,15 +465,17 @@ def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
         outs.append(_ext.w8a16(x, q, None, s, b, torch.bfloat16, GG, "e4m3fn"))
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
-    _check(outs[1], x, q, s, GG, "e4m3fn", b, torch.bfloat16, "gemv", "decode transposed loads")
+    _check(outs[1], x, q, s, GG, "e4m3fn", b, torch.bfloat16, "gemv" if M <= 8 else "gemm",
+           "decode transposed loads")
 
 
 def test_weight_matrix_past_2gib():
     """A weight matrix of more than 2^31 bytes (K=16384, N=132096: 2.16 GB of codes): buffer offsets
     inside every kernel are 32-bit, so the GEMV splits the launch by rows and the GEMMs address the
-    weights per block.  M=1 (GEMV), M=4 (matrix-core decode), M=16 (the weight-streaming kernel
-    declines, the LDS-tiled kernel runs) and M=128 (direct-load GEMM); output columns at both ends
-    of the matrix against the float64 oracle on those rows."""
+    weights per block.  M=1 (GEMV), M=4 and M=16 (matrix-core decode), M=16 with the decode kernel
+    held to 8 rows (the weight-streaming kernel declines, the LDS-tiled kernel runs) and M=128
+    (direct-load GEMM); output columns at both ends of the matrix against the float64 oracle on
+    those rows."""
     K, N = 16384, 132096
     assert N * K > 2 ** 31
     print(f"[linear] N={N} K={K}: {N * K / 2 ** 30:.2f} GiB of codes", flush=True)
@@ -477,9 +486,13 @@ def test_weight_matrix_past_2gib():
     torch.cuda.empty_cache()
     cols = np.r_[0:48, N - 80:N]
     qs, ss = q[cols].cpu().numpy(), s[cols].cpu().numpy()
-    for M in (1, 4, 16, 128):
+    for M, mfma_max in ((1, "16"), (4, "16"), (16, "16"), (16, "8"), (128, "16")):
+        os.environ["TFP8_GEMV_MFMA_MAX_M"] = mfma_max
         x = (torch.randn(M, K, generator=g, device="cuda") * 0.5).bfloat16()
-        y = _ext.w8a16(x, q, None, s, None, torch.float32, G, "e4m3fn")
+        try:
+            y = _ext.w8a16(x, q, None, s, None, torch.float32, G, "e4m3fn")
+        finally:
+            os.environ.pop("TFP8_GEMV_MFMA_MAX_M")
         ref = O.linear_ref64(_x_eff(x, "gemv" if M <= _ext.GEMV_MAXM else "gemm"), qs, ss, G, "e4m3fn", None)
         got = y[:, cols].double().cpu().numpy()
         d = np.abs(got - ref)
