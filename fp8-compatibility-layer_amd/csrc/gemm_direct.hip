@@ -397,11 +397,12 @@ constexpr GdCfg GD_CFGS[] = {
 };
 constexpr int GD_NCFG = (int)(sizeof(GD_CFGS) / sizeof(GD_CFGS[0]));
 
-// Smallest M this kernel takes; the weight-streaming kernel serves fewer rows.  Sweep on MI355X
-// at K = N = 8192 (us, weight-streaming vs this kernel's best configuration): M=16 17.2 vs 22.9,
-// M=32 22.0 vs 24.7, M=64 27.5 vs 26.4, M=128 43.4 vs 33.3 (128 x 128, 6 stages), M=256 56.1
-// (LDS-tiled) vs 50.7 (128 x 256, 4 stages).
-int gd_min_m() { return gd_env_int("TFP8_GEMM_DIRECT_MIN_M", 65); }
+// Smallest M this kernel takes; the weight-streaming kernel serves fewer rows.  Same-box sweep on
+// MI355X at K = N = 8192, per-channel scales (us, weight-streaming vs this kernel's default
+// configuration): M=24 20.2 vs 22.5, M=32 20.9 vs 23.4, M=48 25.3 vs 24.9, M=64 27.6 vs 25.4
+// (64 x 128, 7 stages); M=128 43.4 vs 33.3 (128 x 128, 6 stages); M=256 56.1 (LDS-tiled) vs 51
+// (128 x 256, 4 stages).
+int gd_min_m() { return gd_env_int("TFP8_GEMM_DIRECT_MIN_M", 48); }
 
 GdCfg gd_cfg(int M) {
     int c = M > 128 ? 0 : M > 64 ? 6 : M > 32 ? 7 : 5;
