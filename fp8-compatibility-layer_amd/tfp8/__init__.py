@@ -1,5 +1,6 @@
 """tfp8 on MI355X: FP8 weights (uint8 codes + f32/UE8M0 scales) decoded inside gfx950 kernels --
-a streaming GEMV for M <= 8 and an LDS-tiled MFMA GEMM above -- with fp32 accumulation.
+a streaming GEMV and matrix-core decode kernel for small M, MFMA GEMMs above -- with fp32
+accumulation.
 
 Drop-in for the reference package's API (tfp8/__init__.py:9-16): FP8Config, FP8Linear,
 prepare_model, plan, report, weight_bytes, quantize_weight, dequantize_weight, decode, encode,

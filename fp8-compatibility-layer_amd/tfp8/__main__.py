@@ -36,8 +36,9 @@ def main():
     x = torch.randn(4096) * 100
     enc = encode(x.to(dev), E4M3FN).cpu()
     print(f"  encode RNE matches torch float8 cast: {torch.equal(enc, x.to(torch.float8_e4m3fn).view(torch.uint8))}")
-    print("\nkernels: GEMV (M<=8, dwordx4 stream, in-register cvt decode, DPP reduce),"
-          " MFMA GEMM (M>8, FP8 tile in LDS, f16/bf16 16x16x32 MFMA, fp32 acc)")
+    print("\nkernels: GEMV (M<=3, dwordx4 stream, in-register cvt decode, DPP reduce),"
+          " matrix-core decode (4<=M<=16), MFMA GEMMs (M>16, FP8 tiles in LDS or registers,"
+          " f16/bf16 MFMA, fp32 acc)")
     print("  ABI: qweight uint8[N,K], weight_scale f32|ue8m0[N,K/G], bias f32[N] -- include/tfp8_hip.h")
 
 

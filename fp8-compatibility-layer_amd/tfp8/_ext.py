@@ -233,8 +233,11 @@ def _workspace(device, nbytes):
 def w8a16(x, qweight, lut16, wscale, bias, out_dtype, group_size, fmt="e4m3fn"):
     """y = x @ dequant(qweight).T + bias  (tfp8/_ext.py:230-253).
 
-    M <= 8   streaming GEMV on x in its own dtype (fp32 FMA)
-    M > 8    LDS-tiled MFMA GEMM: f16/bf16 x directly, fp32 x via the fp16 row-scaled prep
+    M <= 8   GEMV path on x in its own dtype: streaming GEMV (dot products, fp32 accumulation) up
+             to 3 rows, the matrix-core decode kernel from 4
+    M > 8    MFMA GEMM path (decode kernel up to 16 rows, then weight-streaming / direct-to-LDS /
+             LDS-tiled by M and scale layout): f16/bf16 x directly, fp32 x via the fp16 row-scaled
+             prep
     `lut16` is accepted for the reference signature and unused.
     """
     lib = require()

@@ -105,7 +105,9 @@ int tfp8_dequant(const uint8_t* w, int N, int K, const void* ws, int ws_kind, in
  *   bias  [N] f32 or NULL
  *   y     [M,N] row-major, y_dtype
  *
- * M <= 8 runs the streaming GEMV; M > 8 runs the LDS-tiled MFMA GEMM, which additionally
+ * M <= 8 runs the GEMV path (the streaming GEMV up to 3 rows, the matrix-core decode kernel
+ * from 4); M > 8 runs the MFMA GEMM path (the decode kernel up to 16 rows, then the
+ * weight-streaming, direct-to-LDS or LDS-tiled GEMM by M and scale layout), which additionally
  * needs G == K or G % 32 == 0.  fp32 activations on the GEMM path are first converted to
  * fp16 with a power-of-two row scale (tfp8_prepare_activations) in the workspace; the GEMM
  * may also split K across blocks and keep fp32 partial sums there.  The needed size is
