@@ -21,6 +21,7 @@
 //     LDS (row stride padded by 16 B, conflict-free ds_read_b128), filled through registers one
 //     chunk ahead; out-of-range weight rows/columns read zeros from the buffer resource.
 #include <algorithm>
+#include <atomic>
 
 #include "tfp8_common.h"
 
@@ -283,15 +284,19 @@ int gs_env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
+// CU count of the current device, queried once per device (host threads may race to fill an
+// entry with the same value, hence the atomic).
 int gs_cus() {
-    static int cus[64];
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (!c) {
         int v = 0;
-        cus[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+        c = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+        cus[dev].store(c, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return c;
 }
 
 }  // namespace

@@ -27,6 +27,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "tfp8_common.h"
 
@@ -344,20 +345,25 @@ static inline int gemv_env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-// Per-device attributes, queried once: CU count and the LDS bytes one block may use.
+// Per-device attributes, queried once: CU count and the LDS bytes one block may use.  Callers on
+// several host threads may fill an entry at the same time (with the same values): the LDS size is
+// stored before the CU count is published (release), and a reader that sees the CU count
+// (acquire) sees the LDS size.
 struct DevInfo { int cus, lds; };
 static inline DevInfo dev_info() {
-    static DevInfo info[64];
+    static std::atomic<int> cus[64], lds[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return {256, 64 * 1024};
-    if (!info[dev].cus) {
+    int c = cus[dev].load(std::memory_order_acquire);
+    if (!c) {
         int v = 0, l = 0;
         const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0;
         const bool okl = hipDeviceGetAttribute(&l, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && l > 0;
-        info[dev].lds = okl ? l : 64 * 1024;
-        info[dev].cus = ok ? v : 256;
+        lds[dev].store(okl ? l : 64 * 1024, std::memory_order_relaxed);
+        c = ok ? v : 256;
+        cus[dev].store(c, std::memory_order_release);
     }
-    return info[dev];
+    return {c, lds[dev].load(std::memory_order_relaxed)};
 }
 
 // Config by shape; sized from a sweep on MI355X.  Every config is correct for every shape.
