@@ -499,3 +499,35 @@ def test_weight_matrix_past_2gib():
         assert (d <= O.tolerance(ref, "float32")).all(), (M, float(d.max()))
     del q, s
     torch.cuda.empty_cache()
+
+
+def test_concurrent_streams_match_serial():
+    """The library keeps no device state between calls: the GEMV, the matrix-core decode kernel
+    and split-K GEMMs (each call with its own workspace from torch's stream-ordered allocator)
+    launched on two streams at once, in opposite orders and several times over, give the same bits
+    as the same calls run one after another on one stream (tfp8/_ext.py:230-253 launches on the
+    caller's current stream)."""
+    g = torch.Generator().manual_seed(5)
+    cases = []
+    for M, N, K, G, sf in [(1, 4096, 4096, 128, "f32"), (8, 2048, 4096, None, "ue8m0"),
+                           (256, 2048, 4096, None, "ue8m0"), (64, 1024, 8192, None, "f32"),
+                           (24, 1536, 4096, 128, "f32")]:
+        q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, seed=M + N)
+        x = torch.randn(M, K, generator=g).bfloat16().cuda()
+        cases.append((x, q, s, GG, b))
+    serial = [_ext.w8a16(x, q, None, s, b, torch.float32, GG, "e4m3fn") for x, q, s, GG, b in cases]
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())   # default priority
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    got = []
+    for rep in range(3):
+        for si, st in enumerate(streams):
+            order = list(range(len(cases))) if si == 0 else list(range(len(cases)))[::-1]
+            with torch.cuda.stream(st):
+                for i in order:
+                    x, q, s, GG, b = cases[i]
+                    got.append((i, _ext.w8a16(x, q, None, s, b, torch.float32, GG, "e4m3fn")))
+    torch.cuda.synchronize()
+    for i, y in got:
+        assert torch.equal(y, serial[i]), f"case {i}: result differs when run on two streams"
