@@ -129,6 +129,13 @@ def _dtype_id(t):
         raise TypeError(f"tfp8 kernels take float16/bfloat16/float32, got {t}") from None
 
 
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    """x itself when its data starts on a 16-byte boundary (what the kernels' 16-byte loads need),
+    else an aligned copy: a contiguous view can start anywhere in its storage (e.g. one row sliced
+    one element in), and the library refuses such a pointer rather than read it misaligned."""
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
 def scale_kind(ws: torch.Tensor) -> int:
     if ws.dtype == torch.float32:
         return SCALE_F32
@@ -247,7 +254,7 @@ def w8a16(x, qweight, lut16, wscale, bias, out_dtype, group_size, fmt="e4m3fn"):
     y = torch.empty(M, N, dtype=out_dtype, device=x.device)
     if M == 0:
         return y
-    x = x.contiguous()
+    x = _aligned(x.contiguous())
     xd = _dtype_id(x.dtype)
     dev = x.get_device()
     nb = lib.tfp8_linear_workspace_size(xd, M, N, K)
@@ -264,7 +271,7 @@ def gemv(x, qweight, wscale, bias, out_dtype, group_size, fmt="e4m3fn"):
     M, K = x.shape
     N = qweight.shape[0]
     _same_device(x, qweight, wscale, bias)
-    x = x.contiguous()
+    x = _aligned(x.contiguous())
     y = torch.empty(M, N, dtype=out_dtype, device=x.device)
     _check(lib.tfp8_gemv(x.data_ptr(), _dtype_id(x.dtype), M, K, qweight.data_ptr(), N, wscale.data_ptr(),
                          scale_kind(wscale), group_size, FMT_ID[fmt], _ptr(bias), y.data_ptr(),

@@ -135,7 +135,7 @@ class FP8Linear(nn.Module):
         # only x's data pointer and M are needed, so an [B, T, K] input is neither reshaped in nor
         # out, and the output is allocated in its final shape.
         if ((self._nan_checks >= 3 or not self.nan_check) and self.fallback is None
-                and self._kernels_ok and x.is_cuda and x.is_contiguous()):
+                and self._kernels_ok and x.is_cuda and x.is_contiguous() and x.data_ptr() % 16 == 0):
             shape = x.shape
             if shape[-1] == self.in_features:
                 M = x.numel() // shape[-1]
@@ -151,6 +151,8 @@ class FP8Linear(nn.Module):
         x2 = x if x.dim() == 2 else x.reshape(-1, shape[-1])
         if not x2.is_contiguous():
             x2 = x2.contiguous()
+        if x2.is_cuda and x2.data_ptr() % 16:
+            x2 = x2.clone()        # the kernels load x 16 bytes at a time
         M = x2.shape[0]
         if not self._kernels_ok or not x2.is_cuda:
             self.stats["torch"] += 1

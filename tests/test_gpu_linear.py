@@ -531,3 +531,23 @@ def test_concurrent_streams_match_serial():
     torch.cuda.synchronize()
     for i, y in got:
         assert torch.equal(y, serial[i]), f"case {i}: result differs when run on two streams"
+
+
+def test_misaligned_contiguous_input():
+    """A contiguous input whose data does not start on a 16-byte boundary (one row sliced one
+    element into its storage, and a flat buffer viewed from element 3): FP8Linear and w8a16 run it
+    through an aligned copy and give the same bits as the aligned input."""
+    torch.manual_seed(11)
+    lin = nn.Linear(512, 192, device="cuda")
+    f = FP8Linear.from_linear(lin)
+    f.out_dtype = torch.float32
+    for M in (1, 4, 40):
+        base = torch.randn(M, 513, device="cuda").bfloat16()
+        xm = base[:, 1:] if M == 1 else torch.randn(M * 512 + 3, device="cuda").bfloat16()[3:].view(M, 512)
+        assert xm.is_contiguous() and xm.data_ptr() % 16
+        xa = xm.clone()
+        for _ in range(4):                      # past the NaN-checked calls: the decode fast path too
+            got, want = f(xm), f(xa)
+            assert torch.equal(got, want), f"M={M}"
+        y = _ext.w8a16(xm, f.qweight, None, f.weight_scale, f.bias_f32, torch.float32, f.group_size, f.fmt)
+        assert torch.equal(y, want)
