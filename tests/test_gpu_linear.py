@@ -5,7 +5,7 @@ oracle, with the reference's tolerance (tests/test_tfp8.py:86-89):
 
 Cases: the reference's kernel gates (switch points, tails, ragged K, group scales x formats x
 dtypes, pipeline edges, folded group scales, empty / non-contiguous / N-d input, prepared GEMV
-launch state, NaN fallback) and every BASELINE config at its full size, plus the reference's
+launch state, NaN fallback) and every benchmark configuration (C1-C4) at its full size, plus the reference's
 CPU dequantize-then-matmul path as a second reference.
 """
 import os
@@ -244,7 +244,7 @@ def test_chunked_backend_counts_and_matches():
                f"chunked N={N}")
 
 
-# ------------------------------------------------------------------ BASELINE configs, full size
+# ------------------------------------------------------------------ benchmark configurations C1-C4, full size
 def test_config1_gemv_m1_and_cpu_path():
     """C1: M=1, K=N=4096, fp16 x ~N(0,1), W ~N(0,0.02) E4M3FN per-channel pow2 f32, no bias."""
     print("[C1] M=1 K=N=4096", flush=True)

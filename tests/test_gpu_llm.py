@@ -1,6 +1,6 @@
 """C5 end to end: the Llama-style decoder (8 layers, d=2048, 16 heads, SwiGLU 5632, vocab 32000,
 random N(0, 0.02) init) converted by prepare_model to E4M3FN per-channel FP8Linear, prefilled with
-512 tokens and greedily decoded for 128 at batch 1 and batch 8.
+512 tokens and greedily decoded for 128 at batch 1 and batch 8 (benchmark configuration C5).
 
 Parity: the same model with every FP8Linear replaced by the reference's CPU forward arithmetic
 (tfp8/linear.py:179-181: fp32 F.linear of the dequantized weight, evaluated as an fp32 GPU matmul)
