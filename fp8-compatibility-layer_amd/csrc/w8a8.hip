@@ -94,9 +94,9 @@ __global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict
 // ------------------------------------------------------------------ GEMM
 // Three kernels share the tiling below and differ in what the matrix cores multiply:
 //
-//   w8_bf16_kernel (default for UE8M0 block scales and row/column scales): each FP8 fragment is
-//     decoded to bf16 right before its MFMA with the UE8M0 block scale folded into the decode
-//     (exact), and v_mfma_f32_16x16x32_bf16 accumulates exact products in fp32.
+//   w8_bf16_kernel (default for UE8M0 block scales and row/column scales): FP8 codes are decoded
+//     to bf16 once per tile with the UE8M0 block scale folded into the decode (exact), and
+//     v_mfma_f32_16x16x32_bf16 accumulates exact products in fp32.
 //   w8_f16_kernel (default for FP32 block scales): FP8 codes are decoded to f16 once per tile
 //     (exact: every FP8 value is an f16) and multiplied by v_mfma_f32_16x16x32_f16, whose products
 //     reach the fp32 accumulator exactly -- the numerics of the reference's fp16 WMMA
@@ -110,9 +110,10 @@ __global__ __launch_bounds__(256) void w8_quantize_kernel(const void* __restrict
 //     v_mfma_f32_16x16x32 per 128-step with the fp32 multiply-accumulate above.
 //
 // Tiling: block tile BT x BT of C split over a grid of waves, each owning TI x TJ MFMA tiles of
-// 16 x 16; K advances 128 per step.  Each step's A and Bt tiles (BT rows x 128 codes,
-// k contiguous) are loaded into registers one step ahead and written (decoded, for the f16
-// kernel) to the other half of a double-buffered LDS pair, so one barrier per step suffices.
+// 16 x 16; K advances 128 per step (64 in the bf16 kernel).  Each step's A and Bt tiles (BT rows
+// x the step's codes, k contiguous) are loaded into registers one step ahead and written (decoded,
+// for the f16 and bf16 kernels) to the other half of a double-buffered LDS pair, so one barrier
+// per step suffices.
 // Out-of-range rows and the K tail read as zero through buffer-load bounds.
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -507,16 +508,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(1, (W8MxCfg<FA, FB, UE8M0,
 }
 
 // ---- exact kernel with scales folded into the decode: UE8M0 block scales and row/column scales.
-// FP8 tiles stay FP8 in LDS (256 x 256 tile, 8 waves of 128 x 64, two per SIMD, as the native
-// kernel).  Each fragment of one 32-wide block is decoded to bf16 right before its MFMA by
-// v_cvt_scalef32_pk_bf16_{fp8,bf8}, whose scale operand carries an E8M0 exponent: with UE8M0 block
-// scales the lane passes 2^(byte-127) (bits byte << 23), so the bf16 value is code * scale exactly
-// (4 or 3 significant bits, and fp32's exponent range, fit bf16 for every product above 2^-126 --
-// scales from the quantizer are >= 2^-40).  Then v_mfma_f32_16x16x32_bf16 accumulates in fp32
-// with exact products: C = sum_kb sum_k (A sa)(B sb), the reference's per-block sum with the
-// scales moved inside, with no per-block multiply-add.  Row/column scales decode with scale 1 and
-// go to the epilogue.  Lane l of an MFMA for block q reads 8 codes of row l & 15 at
-// k = 32q + 8 (l >> 4) (ds_read_b64 from the XOR-swizzled 128-byte rows).
+// Codes are decoded to bf16 by v_cvt_scalef32_pk_bf16_{fp8,bf8}, whose scale operand carries an
+// E8M0 exponent: with UE8M0 block scales the thread passes 2^(byte-127) (bits byte << 23), so the
+// bf16 value is code * scale exactly (4 or 3 significant bits, and fp32's exponent range, fit bf16
+// for every product above 2^-126 -- scales from the quantizer are >= 2^-40).  Then
+// v_mfma_f32_16x16x32_bf16 accumulates in fp32 with exact products: C = sum_kb sum_k (A sa)(B sb),
+// the reference's per-block sum with the scales moved inside, with no per-block multiply-add.
+// Row/column scales decode with scale 1 and go to the epilogue.
 template <int F>
 __device__ __forceinline__ uint32_t w8_cvt_bf16(uint32_t w, float scale, bool hi) {
     bf16x2 v;
@@ -528,72 +526,83 @@ __device__ __forceinline__ uint32_t w8_cvt_bf16(uint32_t w, float scale, bool hi
                : __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, scale, false);
     return __builtin_bit_cast(uint32_t, v);
 }
-template <int F>
-__device__ __forceinline__ bf16x8 w8_frag_bf16(uint2 raw, float scale) {
-    const uint32_t h0 = w8_cvt_bf16<F>(raw.x, scale, false), h1 = w8_cvt_bf16<F>(raw.x, scale, true);
-    const uint32_t h2 = w8_cvt_bf16<F>(raw.y, scale, false), h3 = w8_cvt_bf16<F>(raw.y, scale, true);
-    return __builtin_bit_cast(bf16x8, make_uint4(h0, h1, h2, h3));
-}
-// E8M0 byte q of a scale word, as the f32 whose exponent field is that byte (byte 0 -> 0.0f, whose
-// exponent field 0 is E8M0 2^-127; 255 -> inf, E8M0 NaN).
-__device__ __forceinline__ float w8_e8m0_of(uint32_t word, int q) {
-    return __uint_as_float(((word >> (8 * q)) & 0xFFu) << 23);
-}
 
+// 256 x 256 tile, 8 waves of 128 x 64 (two per SIMD).  Each K step (64 wide) of A and Bt is loaded
+// into registers one step ahead, decoded to bf16 with its block's E8M0 scale folded in and written
+// to the other half of a double-buffered LDS pair (2 x 2 x 32 KB); the waves then read bf16
+// fragments.  Every code is decoded once per block: decoding each wave's fragments right before
+// its MFMAs instead decodes an A code in 4 waves and a Bt code in 2, and ran 10 % slower at 8192^3.
+// LDS rows are 64 bf16 = 128 bytes; 16-byte chunk u of row r sits at u ^ ((r >> 1) & 7), so the
+// 16 rows one fragment read touches land on distinct bank groups.
 template <int FA, int FB, bool UE8M0, int MODE>
 __global__ __launch_bounds__(512) void w8_bf16_kernel(const uint8_t* __restrict__ a, const void* __restrict__ sa,
-                                                      const uint8_t* __restrict__ bt, const void* __restrict__ sb,
-                                                      const float* __restrict__ bias, float* __restrict__ c, int M,
-                                                      int N, int K) {
-    constexpr int BT = 256, WM = 2, WN = 4, NT = 512;
+                                                       const uint8_t* __restrict__ bt, const void* __restrict__ sb,
+                                                       const float* __restrict__ bias, float* __restrict__ c, int M,
+                                                       int N, int K) {
+    constexpr int BT = 256, WM = 2, WN = 4, NT = 512, KT = 64;
     constexpr int WTM = BT / WM, WTN = BT / WN, TI = WTM / 16, TJ = WTN / 16;
+    constexpr int CH = BT * (KT / 16) / NT;   // 16-code chunks per thread and operand
     constexpr bool BLK = MODE == W8_BLOCK;
     static_assert(!BLK || UE8M0, "FP32 block scales cannot be folded into the decode");
-    using L = W8Loader<BT, false, false, NT>;
     __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 128];
-    __shared__ __attribute__((aligned(16))) uint32_t sS[2][2][BLK ? BT : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     int m0, n0;
     w8_tile(M, N, BT, m0, n0);
-    L ld(a, sa, bt, sb, M, N, K, m0, n0);
-    const int nkb = K / 32, ntile = (K + 127) / 128;
-
-    // UE8M0 block scales: per step one word per row (bytes = blocks kb0 .. kb0+3); 2 x 256 words,
-    // one per thread: waves 0-3 take A's rows, waves 4-7 Bt's (the operand is wave-uniform).
-    __amdgpu_buffer_rsrc_t rsu[2];
-    uint32_t rsc8 = 0;
+    const int nkb = K / 32, ntile = (K + KT - 1) / KT;
+    const uint32_t rows[2] = {(uint32_t)min(BT, M - m0), (uint32_t)min(BT, N - n0)};
+    __amdgpu_buffer_rsrc_t rs[2], rss[2];
+    rs[0] = __builtin_amdgcn_make_buffer_rsrc((void*)(a + (size_t)m0 * K), (short)0, (int)(rows[0] * (uint32_t)K),
+                                              (int)W8_FLAGS);
+    rs[1] = __builtin_amdgcn_make_buffer_rsrc((void*)(bt + (size_t)n0 * K), (short)0, (int)(rows[1] * (uint32_t)K),
+                                              (int)W8_FLAGS);
     if constexpr (BLK) {
-        rsu[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb), (short)0,
-                                                   (int)((uint32_t)min(BT, M - m0) * (uint32_t)nkb), (int)W8_FLAGS);
-        rsu[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb), (short)0,
-                                                   (int)((uint32_t)min(BT, N - n0) * (uint32_t)nkb), (int)W8_FLAGS);
+        rss[0] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sa + (size_t)m0 * nkb), (short)0,
+                                                   (int)(rows[0] * (uint32_t)nkb), (int)W8_FLAGS);
+        rss[1] = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)sb + (size_t)n0 * nkb), (short)0,
+                                                   (int)(rows[1] * (uint32_t)nkb), (int)W8_FLAGS);
     }
-    const int s_op = wave >> 2, s_row = (wave & 3) * 64 + lane;
+
+    // Chunk ch = tid + i * NT of an operand: row ch >> 2, codes k = kt + 16 (ch & 3) .. +15, all in
+    // scale block (kt + 16 (ch & 3)) / 32.  Past K (and past the rows of the block) the loads read
+    // zeros; a zero scale byte decodes zero codes to zero.
+    uint4 rt[2][CH];
+    uint32_t rsb[2][CH];
     auto load = [&](int kt) {
-        ld.load(kt, tid);
-        if constexpr (BLK) {
-            const int kb0 = kt / 32;
-            uint32_t v = 0;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint32_t o = kb0 + b < nkb ? (uint32_t)(s_row * nkb + kb0 + b) : W8_OOB;
-                v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rsu[s_op], (int)o, 0, 0) << (8 * b);
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int ch = tid + i * NT, row = ch >> 2, k = kt + 16 * (ch & 3);
+                const uint32_t off = k < K ? (uint32_t)row * (uint32_t)K + (uint32_t)k : W8_OOB;
+                rt[op][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)off, 0, 0));
+                if constexpr (BLK) {
+                    const uint32_t o = k < K ? (uint32_t)(row * nkb + k / 32) : W8_OOB;
+                    rsb[op][i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rss[op], (int)o, 0, 0);
+                }
             }
-            rsc8 = v;
-        }
     };
     auto store = [&](int buf) {
 #pragma unroll
         for (int op = 0; op < 2; ++op)
 #pragma unroll
-            for (int i = 0; i < L::CH; ++i) {
-                const int ch = tid + i * NT, row = ch >> 3, cc = ch & 7, sw = (row >> 1) & 7;
-                *(uint4*)&sT[buf][op][row * 128 + 16 * (cc ^ sw)] = ld.rt[op][i];
+            for (int i = 0; i < CH; ++i) {
+                const int ch = tid + i * NT, row = ch >> 2, u = 2 * (ch & 3), sw = (row >> 1) & 7;
+                const float s = BLK ? __uint_as_float(rsb[op][i] << 23) : 1.f;
+                const uint4 v = rt[op][i];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+                uint32_t h[8];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    h[2 * d] = op == 0 ? w8_cvt_bf16<FA>(w[d], s, false) : w8_cvt_bf16<FB>(w[d], s, false);
+                    h[2 * d + 1] = op == 0 ? w8_cvt_bf16<FA>(w[d], s, true) : w8_cvt_bf16<FB>(w[d], s, true);
+                }
+                uint8_t* base = &sT[buf][op][row * 128];
+                *(uint4*)(base + 16 * (u ^ sw)) = make_uint4(h[0], h[1], h[2], h[3]);
+                *(uint4*)(base + 16 * ((u + 1) ^ sw)) = make_uint4(h[4], h[5], h[6], h[7]);
             }
-        if constexpr (BLK) sS[buf][s_op][s_row] = rsc8;
     };
 
     f32x4 acc[TI][TJ];
@@ -602,10 +611,11 @@ __global__ __launch_bounds__(512) void w8_bf16_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int frow = lane & 15, g = lane >> 4, sw = (frow >> 1) & 7;
-    // 8 codes of block q of a row for this lane: logical chunk 2q + (g >> 1), half g & 1
-    auto raw8 = [&](int buf, int op, int row, int q) -> uint2 {
-        return *(const uint2*)&sT[buf][op][row * 128 + 16 * ((2 * q + (g >> 1)) ^ sw) + 8 * (g & 1)];
+    // Lane l of an MFMA for block q of the step reads row l & 15, k = 32q + 8 (l >> 4) .. +7:
+    // logical chunk 4q + (l >> 4).
+    const int frow = lane & 15, g = lane >> 4, fsw = (frow >> 1) & 7;
+    auto frag = [&](int buf, int op, int row, int q) -> bf16x8 {
+        return *(const bf16x8*)&sT[buf][op][row * 128 + 16 * ((4 * q + g) ^ fsw)];
     };
 
     load(0);
@@ -613,24 +623,15 @@ __global__ __launch_bounds__(512) void w8_bf16_kernel(const uint8_t* __restrict_
     __syncthreads();
     for (int t = 0; t < ntile; ++t) {
         const int buf = t & 1;
-        if (t + 1 < ntile) load((t + 1) * 128);
-        uint32_t swa[TI], swb[TJ];   // scale words of this lane's rows and columns
-        if constexpr (BLK) {
+        if (t + 1 < ntile) load((t + 1) * KT);
 #pragma unroll
-            for (int i = 0; i < TI; ++i) swa[i] = sS[buf][0][wm * WTM + i * 16 + frow];
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) swb[j] = sS[buf][1][wn * WTN + j * 16 + frow];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {   // blocks past K hold zero codes (scale byte 0: finite)
+        for (int q = 0; q < KT / 32; ++q) {
             bf16x8 bd[TJ];
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
-                bd[j] = w8_frag_bf16<FB>(raw8(buf, 1, wn * WTN + j * 16 + frow, q), BLK ? w8_e8m0_of(swb[j], q) : 1.f);
+            for (int j = 0; j < TJ; ++j) bd[j] = frag(buf, 1, wn * WTN + j * 16 + frow, q);
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const bf16x8 ad =
-                    w8_frag_bf16<FA>(raw8(buf, 0, wm * WTM + i * 16 + frow, q), BLK ? w8_e8m0_of(swa[i], q) : 1.f);
+                const bf16x8 ad = frag(buf, 0, wm * WTM + i * 16 + frow, q);
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, bd[j], acc[i][j], 0, 0, 0);
             }
