@@ -11,6 +11,8 @@
 // The weight operand is taken transposed, Bt[N,K] (k contiguous, as the quantizer writes it):
 // both matrix-core operands then load as contiguous k runs.  The GEMM kernels and their numerics
 // are described at the GEMM section below.
+#include <type_traits>
+
 #include "tfp8_common.h"
 
 namespace tfp8 {
@@ -302,12 +304,12 @@ __global__ __launch_bounds__(512) void w8_f16_kernel(
         return *(const f16x8*)&sT[buf][op][row * 128 + 16 * ((4 * q + g) ^ fsw)];
     };
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int t = 0; t < ntile; ++t) {
+    // K step t; MORE: step t + 1 exists, so its tile is loaded during this step and stored after it.
+    // The steady state runs with MORE constant, without branches around the loads and LDS writes.
+    auto step = [&](int t, auto more_c) {
+        constexpr bool MORE = decltype(more_c)::value;
         const int buf = t & 1;
-        if (t + 1 < ntile) load((t + 1) * KS);
+        if constexpr (MORE) load((t + 1) * KS);
         f16x8 bf[TJ][2];
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
@@ -338,9 +340,15 @@ __global__ __launch_bounds__(512) void w8_f16_kernel(
                 }
             }
         }
-        if (t + 1 < ntile) store(buf ^ 1);
+        if constexpr (MORE) store(buf ^ 1);
         __syncthreads();
-    }
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    int t = 0;
+    for (; t + 1 < ntile; ++t) step(t, std::true_type{});
+    step(t, std::false_type{});
     w8_store<TI, TJ, WTM, WTN, false, W8_BLOCK>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
@@ -649,6 +657,8 @@ __global__ __launch_bounds__(512) void w8_bf16_kernel(const uint8_t* __restrict_
         return *(const bf16x8*)&sT[buf][op][row * 128 + 16 * ((4 * q + g) ^ fsw)];
     };
 
+    // The loop keeps its conditional load and store: with the steady state split off branch-free
+    // (as the f16 kernel does) this kernel ran 5 % slower (1285 vs 1219 us at 8192^3).
     load(0);
     store(0);
     __syncthreads();
