@@ -55,9 +55,10 @@ __global__ __launch_bounds__(EW_THREADS) void encode_kernel(const void* __restri
 
 // ------------------------------------------------------------------ quantize_weight
 // One wave per (row n, K-group g), four groups per block: group amax (NaN propagates, as
-// torch.amax does), scale s = max(amax/max_finite, FLT_MIN), exact power-of-two ceiling when
-// requested, s = 1 for an all-zero group, then q = encode(w / s) (the encoder saturates, which
-// equals clamp-then-RNE of tfp8/quantize.py:29-35).  UE8M0 stores ceil(log2 s) + 127.
+// torch.amax does), scale s = max(amax/max_finite, FLT_MIN), the power-of-two ceiling of
+// tfp8/quantize.py:11-12 when requested (pow2_ceil_ref: the rounding of torch's fp32 log2), s = 1
+// for an all-zero group, then q = encode(w / s) (the encoder saturates, which equals
+// clamp-then-RNE of tfp8/quantize.py:29-35).  UE8M0 stores log2 of that power of two + 127.
 template <int FMT, int XDT, int SK>
 __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ w, int N, int K, int G,
                                                        int ng, int pow2, uint8_t* __restrict__ q,
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
         s = __uint_as_float(0x7FC00000u);
     } else {
         s = fmaxf(amax / Fmt<FMT>::MAX_FINITE, FLT_MIN);
-        if (pow2 || SK == TFP8_SCALE_UE8M0) s = pow2_ceil_exact(s);
+        if (pow2 || SK == TFP8_SCALE_UE8M0) s = pow2_ceil_ref(s);
         if (amax == 0.f) s = 1.f;
     }
     for (int k = lane; k < G; k += 64) q[base + k] = (uint8_t)encode_fp8<FMT>(load_elem<XDT>(w, base + k) / s);
@@ -103,8 +104,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
 }
 
 // ------------------------------------------------------------------ prepare_activations
-// One block per row.  e = ceil(log2(max(amax, 2^-100))) - 8 from the exponent bits (exact),
-// 0 when amax == 0 (tfp8/quantize.py:54-58); x16 = fp16(x * 2^-e), xs = 2^e.
+// One block per row.  e = ceil(log2(max(amax, 2^-100))) - 8 with the rounding of torch's fp32
+// log2 (ceil_log2_ref), 0 when amax == 0 (tfp8/quantize.py:54-61); x16 = fp16(x * 2^-e), xs = 2^e.
 template <int XDT>
 __global__ __launch_bounds__(256) void prep_kernel(const void* __restrict__ x, int K,
                                                    uint16_t* __restrict__ x16, float* __restrict__ xs) {
@@ -119,10 +120,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const void* __restrict__ x, i
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int e = 0;
     if (amax > 0.f) {
-        const uint32_t b = __float_as_uint(fmaxf(amax, 0x1p-100f));
-        int ex = (int)((b >> 23) & 0xFF) - 127;
-        if (b & 0x007FFFFFu) ex += 1;
-        e = ex - 8;   // ACT_TARGET_EXP
+        e = ceil_log2_ref(fmaxf(amax, 0x1p-100f)) - 8;   // ACT_TARGET_EXP
     }
     const float inv = __uint_as_float((uint32_t)(127 - e) << 23);   // 2^-e, e in [-108, 121]
     for (int k = threadIdx.x; k < K; k += 256) x16[row + k] = f32_to_f16_bits(load_elem<XDT>(x, row + k) * inv);

@@ -430,11 +430,6 @@ struct GemmPlan {
     int slices;               // split-K factor (1 = none)
 };
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 static const GemmPlan GEMM_CFGS[] = {
     {0, 0, 0, 0, 0, 1},
     {16, 64, 1, 4, 64, 1},  {32, 64, 2, 2, 64, 1},   {64, 64, 2, 2, 64, 1},    {64, 128, 2, 2, 64, 1},
@@ -455,13 +450,13 @@ GemmPlan gemm_plan(int M, int N, int K, bool grouped) {
     else if (M <= 64) p = GEMM_CFGS[3];
     else if (M <= 128) p = GEMM_CFGS[4];
     else p = grouped ? GEMM_CFGS[7] : GEMM_CFGS[13];
-    const int forced = env_int("TFP8_GEMM_TILE", 0);   // tuning hook: index into GEMM_CFGS
+    const int forced = tune(TUNE_GEMM_TILE);   // knob TFP8_GEMM_TILE: index into GEMM_CFGS
     if (forced > 0 && forced < GEMM_NCFG) p = GEMM_CFGS[forced];
     const long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const long want = p.wm * p.wn == 8 ? 256 : 512;
     int s = 1;
     while (tiles * s < want && s < 8 && (K / (s * 2)) >= 1024) s *= 2;
-    const int fs = env_int("TFP8_GEMM_SPLITK", 0);
+    const int fs = tune(TUNE_GEMM_SPLITK);
     if (fs > 0) s = std::min(fs, 8);
     p.slices = s;
     return p;
@@ -570,14 +565,14 @@ int run_gemm(const void* x16, int x16_dtype, const float* xs, int M, int K, cons
     // weight-streaming kernel at every M from 9 to 16: C3 M=16 15.7 vs 16.9 us, C2 M=16 16.7 vs
     // 20.7 us); then the direct-to-LDS GEMM (one scale per weight row, from its minimum M up), the
     // weight-streaming kernel (M <= 128) and the LDS-tiled kernel below, the general path.
-    if (M <= env_int("TFP8_GEMV_MFMA_MAX_M", 16) && M >= gemv_mfma_min_m()) {
+    if (M <= tune(TUNE_GEMV_MFMA_MAX_M) && M >= gemv_mfma_min_m()) {
         const int rm = run_gemv_mfma(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
-        if (rm != 1) return rm;
+        if (rm != NOT_TAKEN) return rm;
     }
     const int rd = run_gemm_direct(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
-    if (rd != 1) return rd;
+    if (rd != NOT_TAKEN) return rd;
     const int rs = run_gemm_stream(x16, x16_dtype, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, partial, s);
-    if (rs != 1) return rs;
+    if (rs != NOT_TAKEN) return rs;
     const int ng = K / G;
     GemmPlan p = gemm_plan(M, N, K, ng > 1);
     int slices = p.slices, slice_len = K;

@@ -372,11 +372,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     }
 }
 
-int gd_env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 }  // namespace
 
 namespace {
@@ -402,11 +397,11 @@ constexpr int GD_NCFG = (int)(sizeof(GD_CFGS) / sizeof(GD_CFGS[0]));
 // configuration): M=24 20.2 vs 22.5, M=32 20.9 vs 23.4, M=48 25.3 vs 24.9, M=64 27.6 vs 25.4
 // (64 x 128, 7 stages); M=128 43.4 vs 33.3 (128 x 128, 6 stages); M=256 56.1 (LDS-tiled) vs 51
 // (128 x 256, 4 stages).
-int gd_min_m() { return gd_env_int("TFP8_GEMM_DIRECT_MIN_M", 48); }
+int gd_min_m() { return tune(TUNE_GEMM_DIRECT_MIN_M); }
 
 GdCfg gd_cfg(int M) {
     int c = M > 128 ? 0 : M > 64 ? 6 : M > 32 ? 7 : 5;
-    const int f = gd_env_int("TFP8_GEMM_DCFG", -1);   // tuning hook: index into GD_CFGS
+    const int f = tune(TUNE_GEMM_DCFG);   // knob TFP8_GEMM_DCFG: index into GD_CFGS
     if (f >= 0 && f < GD_NCFG) c = f;
     return GD_CFGS[c];
 }
@@ -424,13 +419,13 @@ static int gd_mode(int K, int G, int ws_kind, int x16_dtype) {
 // Split of K: slices of whole 64-wide steps until the grid has a block per CU, slices of at least
 // 1024.  Depends on the shape only (the workspace is sized from it).
 static bool gd_split(int M, int N, int K, int* slices, int* slice_len) {
-    if (K % GD_BK != 0 || M < gd_min_m() || !gd_env_int("TFP8_GEMM_DIRECT", 1)) return false;
+    if (K % GD_BK != 0 || M < gd_min_m() || !tune(TUNE_GEMM_DIRECT)) return false;
     const GdCfg c = gd_cfg(M);
     if ((long)c.bn * K >= (1L << 31) || (long)c.bm * K * 2 >= (1L << 31)) return false;
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     int s = 1;
     while (tiles * s < 256 && s < 8 && K / (s * 2) >= 1024) s *= 2;
-    const int fs = gd_env_int("TFP8_GEMM_SPLITK", 0);
+    const int fs = tune(TUNE_GEMM_SPLITK);
     if (fs > 0) s = std::min(fs, 8);
     int len = ((K + s - 1) / s + GD_BK - 1) / GD_BK * GD_BK;
     s = (K + len - 1) / len;
@@ -508,7 +503,7 @@ static void gd_launch_mode(int mode, int slices, int slice_len, size_t dyn, cons
         gd_launch<T, FMT, GD_CHANNEL>(slices, slice_len, dyn, x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, part, s);
 }
 
-// Runs this GEMM if it takes the shape; returns 1 if it did not (caller falls back), 0 or an
+// Runs this GEMM if it takes the shape; returns NOT_TAKEN if it did not (caller falls back), 0 or an
 // error code otherwise.  x16 is f16/bf16 [M,K]; partial is the caller's workspace, at least
 // gemm_direct_partial_bytes(M, N, K) bytes.
 int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
@@ -516,7 +511,7 @@ int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int 
                     float* partial, hipStream_t s) {
     int slices, slice_len, mode;
     size_t dyn;
-    if (!gd_plan(M, N, K, G, ws_kind, x16_dtype, &slices, &slice_len, &mode, &dyn)) return 1;
+    if (!gd_plan(M, N, K, G, ws_kind, x16_dtype, &slices, &slice_len, &mode, &dyn)) return NOT_TAKEN;
     float* part = slices > 1 ? partial : nullptr;
     if (x16_dtype == TFP8_BF16) {
         TFP8_DISPATCH_FMT(fmt, F, gd_launch_mode<__bf16, F>(mode, slices, slice_len, dyn, x16, xs, w, ws, ws_kind,

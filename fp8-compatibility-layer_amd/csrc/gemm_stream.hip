@@ -279,11 +279,6 @@ namespace {
 
 struct GsCfg { int tm, nw, kcs; };
 
-int gs_env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 // CU count of the current device, queried once per device (host threads may race to fill an
 // entry with the same value, hence the atomic).
 int gs_cus() {
@@ -322,7 +317,7 @@ void gemm_stream_plan(int M, int N, int K, int G, int gmode, int* tm, int* nw, i
     else if (T > 2) { NWv = 2; KCSv = 2; }
     else if (T > 1) { NWv = 2; KCSv = 4; }
     T = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8;   // callers take this kernel only for M <= GS_MAX_M
-    const int f_nw = gs_env_int("TFP8_GS_NW", 0), f_kcs = gs_env_int("TFP8_GS_KCS", 0);
+    const int f_nw = tune(TUNE_GS_NW), f_kcs = tune(TUNE_GS_KCS);
     if (f_nw) NWv = f_nw;
     if (f_kcs) KCSv = f_kcs;
     const int KC = KCSv * 64;
@@ -334,7 +329,7 @@ void gemm_stream_plan(int M, int N, int K, int G, int gmode, int* tm, int* nw, i
     int s = 1;
     const int want = 2 * gs_cus();
     while (ntile * s * 2 <= want && s < 8 && (K / (s * 2)) >= 2 * KC) s *= 2;
-    const int fs = gs_env_int("TFP8_GS_SPLITK", 0);
+    const int fs = tune(TUNE_GS_SPLITK);
     if (fs > 0) s = std::min(fs, 8);
     int len = ((K + s - 1) / s + align - 1) / align * align;
     s = (K + len - 1) / len;
@@ -356,9 +351,9 @@ static void gs_launch(int slices, int slice_len, const void* x, const float* xs,
     dim3 grid((N + 64 * NW - 1) / (64 * NW), slices);
     const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
     // 256-code chunks load as 4 rows x 256 contiguous bytes per instruction and are regrouped in LDS
-    // (TFP8_GS_TL=0 keeps the 16 rows x 64 bytes operand layout).
+    // (knob TFP8_GS_TL=0 keeps the 16 rows x 64 bytes operand layout).
     if constexpr (KCS == 4) {
-        if (gs_env_int("TFP8_GS_TL", 1)) {
+        if (tune(TUNE_GS_TL)) {
             gemm_stream_kernel<T, FMT, TM, NW, KCS, GMODE, true><<<grid, 256, 0, s>>>(
                 (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, part, slice_len, N);
             return;
@@ -387,13 +382,13 @@ static bool gs_dispatch(int tm, int nw, int kcs, int slices, int slice_len, cons
 void splitk_reduce_launch(const float* part, int S, int M, int N, const void* ws, int sk, int colscale, const float* xs,
                           const float* bias, void* y, int ydt, int xcw, hipStream_t s);
 
-// Runs the streaming GEMM if it takes this shape; returns 1 if it did not (caller falls back),
+// Runs the streaming GEMM if it takes this shape; returns NOT_TAKEN if it did not (caller falls back),
 // 0 or an error code otherwise. x16 is f16/bf16 [M,K]; the matrix must be below 2^31 bytes.
 int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int K, const uint8_t* w, int N,
                     const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
                     float* partial, hipStream_t s) {
     const int gm = gemm_stream_gmode(K, G, ws_kind);
-    if (gm < 0 || M > GS_MAX_M || (long)N * K >= (1L << 31) || gs_env_int("TFP8_GEMM_V1", 0)) return 1;
+    if (gm < 0 || M > GS_MAX_M || (long)N * K >= (1L << 31) || tune(TUNE_GEMM_V1)) return NOT_TAKEN;
     int tm, nw, kcs, slices, slice_len;
     gemm_stream_plan(M, N, K, G, gm, &tm, &nw, &kcs, &slices, &slice_len);
     float* part = slices > 1 ? partial : nullptr;
@@ -412,7 +407,7 @@ int run_gemm_stream(const void* x16, int x16_dtype, const float* xs, int M, int 
             else ok = gs_dispatch<_Float16, F, GM_F32>(tm, nw, kcs, slices, slice_len, x16, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, part, s);
         });
     }
-    if (!ok) return 1;
+    if (!ok) return NOT_TAKEN;
     int rc = check_launch("tfp8_gemm (stream)");
     if (rc || slices <= 1) return rc;
     const int nblk = (N + 64 * nw - 1) / (64 * nw);

@@ -1,7 +1,5 @@
 // GEMV entry: validated by the caller (linear.hip), 1 <= M <= 8; dispatch by activation dtype.
 // The kernel and its launch configurations are in gemv_impl.h.
-#include <stdlib.h>
-
 #include "tfp8_common.h"
 
 namespace tfp8 {
@@ -18,17 +16,14 @@ int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, con
 
 // Smallest M that goes to the matrix-core decode kernel (gemv_mfma.hip); below it the streaming
 // GEMV's per-row dot products are cheaper (measured on MI355X: C2 M=2 12.5 vs 17.1 us, M=4
-// 19.3 vs 17.9 us, M=8 35.2 vs 19.2 us).  TFP8_GEMV_MFMA_MIN overrides (tuning).
-int gemv_mfma_min_m() {
-    const char* e = getenv("TFP8_GEMV_MFMA_MIN");
-    return e && *e ? atoi(e) : 4;
-}
+// 19.3 vs 17.9 us, M=8 35.2 vs 19.2 us).  Knob TFP8_GEMV_MFMA_MIN (default 4).
+int gemv_mfma_min_m() { return tune(TUNE_GEMV_MFMA_MIN); }
 
 int run_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind, int G,
              int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
     if (M >= gemv_mfma_min_m()) {
         const int rc = run_gemv_mfma(x, x_dtype, nullptr, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
-        if (rc != 1) return rc;
+        if (rc != NOT_TAKEN) return rc;
     }
     const int ng = K / G;
     int gshift = -1;

@@ -24,8 +24,6 @@
 //   * a row group is reduced with 4 DPP adds per 16-lane row (quad_perm x2, row_half_mirror,
 //     row_mirror) and 4 v_readlane.
 #pragma once
-#include <stdlib.h>
-
 #include <algorithm>
 #include <atomic>
 
@@ -330,7 +328,7 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
 }
 
 // Compiled configurations (id, R, U, waves per CU, threads per block); gemv_pick() chooses one
-// by shape and TFP8_GEMV_CFG=<id> overrides it.
+// by shape and the knob TFP8_GEMV_CFG=<id> overrides it.
 #ifdef TFP8_GEMV_SWEEP
 #define TFP8_GEMV_CFG_LIST X(0, 1, 2, 32, 256) X(1, 1, 2, 64, 256) X(2, 1, 2, 64, 512) X(3, 1, 2, 64, 1024) \
     X(4, 2, 2, 32, 256) X(5, 2, 2, 32, 1024) X(6, 1, 4, 32, 1024) X(7, 4, 2, 16, 256) X(8, 2, 4, 16, 512) \
@@ -339,11 +337,6 @@ __global__ __launch_bounds__(TPB) void gemv_kernel(
 #else
 #define TFP8_GEMV_CFG_LIST X(2, 1, 2, 64, 512) X(4, 2, 2, 32, 256) X(8, 2, 4, 16, 512) X(17, 2, 2, 28, 448)
 #endif
-
-static inline int gemv_env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
 
 // Per-device attributes, queried once: CU count and the LDS bytes one block may use.  Callers on
 // several host threads may fill an entry at the same time (with the same values): the LDS size is
@@ -368,7 +361,7 @@ static inline DevInfo dev_info() {
 
 // Config by shape; sized from a sweep on MI355X.  Every config is correct for every shape.
 static inline int gemv_pick(int M, int N) {
-    const int forced = gemv_env_int("TFP8_GEMV_CFG", -1);
+    const int forced = tune(TUNE_GEMV_CFG);
     if (forced >= 0) return forced;
     (void)N;
     if (M <= 1) return 4;
@@ -380,7 +373,7 @@ template <int MT, int XDT, int FMT, bool GROUPED, int R, int U, int TPB>
 static void launch_rows(int waves_per_cu, const void* x, const uint8_t* w, const void* ws, int sk, const float* bias,
                         void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int ldy, hipStream_t s) {
     const int ngr = (N + R - 1) / R;
-    const int wpc = gemv_env_int("TFP8_GEMV_WPC", waves_per_cu);
+    const int wpc = tune(TUNE_GEMV_WPC) > 0 ? tune(TUNE_GEMV_WPC) : waves_per_cu;
     const DevInfo di = dev_info();
     long waves = (long)di.cus * wpc;
     if (waves > ngr) waves = ngr;
@@ -396,10 +389,7 @@ static void launch_rows(int waves_per_cu, const void* x, const uint8_t* w, const
     const size_t xbytes = (size_t)M * K * (XDT == TFP8_F32 ? 4 : 2);
     const size_t sbytes = ((size_t)per_block * R * (GROUPED ? ng : 1) * 4 + 15) / 16 * 16;
     const size_t obytes = (size_t)per_block * R * 4;   // bias
-    bool xlds = xbytes + sbytes + obytes <= (size_t)di.lds;
-#ifdef TFP8_GEMV_SWEEP
-    if (gemv_env_int("TFP8_GEMV_XG", 0)) xlds = false;
-#endif
+    const bool xlds = xbytes + sbytes + obytes <= (size_t)di.lds;
     const int xl = xlds ? (int)xbytes : 0;
     if (xlds)
         gemv_kernel<MT, XDT, FMT, GROUPED, R, U, TPB, true><<<grid, TPB, xl + sbytes + obytes, s>>>(

@@ -255,11 +255,6 @@ static void gm_launch(const void* x, const float* xs, const uint8_t* w, const vo
     }
 }
 
-static int gm_env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 template <typename T, int FMT, int SMODE>
 static void gm_pick(int NT, int W, int D, const void* x, const float* xs, const uint8_t* w, const void* ws, int sk,
                     const float* bias, void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int sbytes,
@@ -278,25 +273,25 @@ static void gm_pick(int NT, int W, int D, const void* x, const float* xs, const 
 
 }  // namespace
 
-// Validated by the caller (K % 16, G % 16, K % G, 16-byte aligned x and w).  Returns 1, launching
+// Validated by the caller (K % 16, G % 16, K % G, 16-byte aligned x and w).  Returns NOT_TAKEN, launching
 // nothing, where this kernel does not apply: fp32 activations, M outside 1..16, or f32 K-group
 // scales whose groups are not whole 64-byte chunks.
 int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, const uint8_t* w, int N, const void* ws,
                   int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
-    if (x_dtype == TFP8_F32 || M < 1 || M > 16) return 1;
+    if (x_dtype == TFP8_F32 || M < 1 || M > 16) return NOT_TAKEN;
     const int ng = K / G;
     const int sm = ng == 1 ? SM_CHANNEL : ws_kind == TFP8_SCALE_UE8M0 ? SM_UE8M0 : SM_F32;
-    if (sm == SM_F32 && G % 64) return 1;
+    if (sm == SM_F32 && G % 64) return NOT_TAKEN;
     const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
     // Config: two 16-row weight tiles per block, K split over 4 waves, 4 chunks in flight per wave
-    // (sweep on MI355X at C2 M=4/8; TFP8_GM_NT / _W / _D override, for tuning).
-    const int NT = gm_env_int("TFP8_GM_NT", 2), W = gm_env_int("TFP8_GM_W", 4), D = gm_env_int("TFP8_GM_D", 4);
+    // (sweep on MI355X at C2 M=4/8; knobs TFP8_GM_NT / _W / _D).
+    const int NT = tune(TUNE_GM_NT), W = tune(TUNE_GM_W), D = tune(TUNE_GM_D);
     const int sbytes = sm == SM_CHANNEL ? 0 : (16 * NT * ng * (sm == SM_F32 ? 4 : 1) + 15) / 16 * 16;
     // Transposed weight loads (C2 M=4: 18.1 -> 15.0 us, M=8: 19.4 -> 15.4 us; identical results)
-    // need whole 256-code groups in every wave's K range; TFP8_GM_TL=0 keeps the direct layout.
-    bool tl = gm_env_int("TFP8_GM_TL", 1) != 0 && D % 4 == 0 && K % (256 * W) == 0;
+    // need whole 256-code groups in every wave's K range; knob TFP8_GM_TL=0 keeps the direct layout.
+    bool tl = tune(TUNE_GM_TL) != 0 && D % 4 == 0 && K % (256 * W) == 0;
     if (tl && sbytes + W * NT * (1024 + 4096) > 64 * 1024) tl = false;   // transpose tiles do not fit
-    if (sbytes + W * NT * 1024 > 64 * 1024) return 1;                      // scales of the block's rows
+    if (sbytes + W * NT * 1024 > 64 * 1024) return NOT_TAKEN;                      // scales of the block's rows
 #define TFP8_GM_SM(T_, F_)                                                                                    \
     {                                                                                                         \
         if (sm == SM_CHANNEL) gm_pick<T_, F_, SM_CHANNEL>(NT, W, D, x, xs, w, ws, ws_kind, bias, y, y_dtype, M, N, K, G, ng, gshift, sbytes, tl, s); \

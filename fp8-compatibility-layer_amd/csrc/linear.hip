@@ -52,6 +52,12 @@ extern "C" size_t tfp8_linear_workspace_size(int x_dtype, int M, int N, int K) {
     return b;
 }
 
+extern "C" size_t tfp8_gemm_prepared_workspace_size(int x16_dtype, int M, int N, int K) {
+    (void)x16_dtype;
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return gemm_partial_bytes(M, N, K);
+}
+
 extern "C" int tfp8_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws,
                          int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, void* stream) {
     clear_error();

@@ -29,6 +29,20 @@ int check_launch(const char* what);
 // Clears the thread's last-error message at the start of an entry point.
 void clear_error();
 
+// ------------------------------------------------------------------ tuning knobs (tuning.hip)
+// Kernel-selection overrides, read from the environment once at library load and changed only
+// through tfp8_tuning_set(); the launch path reads them with tune(), never with getenv.
+enum Tune {
+    TUNE_GEMV_CFG, TUNE_GEMV_WPC, TUNE_GEMV_MFMA_MIN, TUNE_GEMV_MFMA_MAX_M, TUNE_GM_NT, TUNE_GM_W, TUNE_GM_D,
+    TUNE_GM_TL, TUNE_GEMM_TILE, TUNE_GEMM_SPLITK, TUNE_GEMM_DIRECT, TUNE_GEMM_DIRECT_MIN_M, TUNE_GEMM_DCFG,
+    TUNE_GS_NW, TUNE_GS_KCS, TUNE_GS_SPLITK, TUNE_GS_TL, TUNE_GEMM_V1, TUNE_COUNT
+};
+int tune(Tune k);
+
+// Returned by a kernel family's run_* function when it does not take the shape (the caller then
+// tries the next family).  Distinct from 0, from every TFP8_ERR_* code and from every hipError_t.
+constexpr int NOT_TAKEN = -1000;
+
 // ------------------------------------------------------------------ format constants
 template <int FMT> struct Fmt;
 template <> struct Fmt<TFP8_E4M3FN> {
@@ -156,12 +170,36 @@ __device__ __forceinline__ float load_scale(const void* ws, size_t i) {
     else return ((const float*)ws)[i];
 }
 
-// Exact 2^ceil(log2 s) for a positive normal f32 (inf and NaN pass through).
-__device__ __forceinline__ float pow2_ceil_exact(float s) {
+// ceil(log2 s) exactly as a correctly rounded fp32 log2 followed by ceil computes it -- the
+// formula torch.exp2(torch.ceil(torch.log2(s))) of tfp8/quantize.py:11-12 and :58-59 -- for a
+// positive normal finite f32 s.  With s = 2^k (1 + j 2^-23), j > 0, the true log2 is
+// k + log2(1 + j 2^-23); it rounds to exactly k, and the ceiling is then k instead of k + 1, when
+// log2(1 + j 2^-23) is below half the gap from k to the next f32 value toward +inf.  That gap is
+// 2^(floor(log2|k|) - 23), or half that for a negative k that is a power of two (the next value
+// toward zero lies in the binade below).  Since log2(1 + f) = f / ln2 to within a relative 1e-5
+// here, the condition is j <= floor(ln2 * 2^p) with p = floor(log2 gap) + 22, which is 0 for
+// |k| < 4 and at most 22 (|k| >= 64).  Checked for every k and j <= 80 against torch's log2.
+__device__ __forceinline__ int ceil_log2_ref(float s) {
+    const uint32_t b = __float_as_uint(s);
+    const int k = (int)((b >> 23) & 0xFF) - 127;
+    const uint32_t j = b & 0x007FFFFFu;
+    if (j == 0u) return k;
+    if (k == 0) return 1;
+    const int ak = k < 0 ? -k : k;
+    int fl = 31 - __builtin_clz((unsigned)ak);        // floor(log2 |k|), 0..6
+    if (k < 0 && (ak & (ak - 1)) == 0) fl -= 1;
+    // floor(ln2 * 2^p) for p = fl - 1 = -2 .. 5
+    constexpr uint32_t JMAX[8] = {0u, 0u, 0u, 1u, 2u, 5u, 11u, 22u};
+    return j <= JMAX[fl + 1] ? k : k + 1;
+}
+
+// 2^ceil(log2 s) with the rounding of ceil_log2_ref (inf and NaN pass through; s positive and
+// normal otherwise, as every caller clamps it to >= FLT_MIN first).
+__device__ __forceinline__ float pow2_ceil_ref(float s) {
     const uint32_t b = __float_as_uint(s);
     if ((b & 0x7F800000u) == 0x7F800000u) return s;
-    if ((b & 0x007FFFFFu) == 0u) return s;
-    return __uint_as_float((b & 0x7F800000u) + 0x00800000u);
+    const int e = ceil_log2_ref(s);
+    return e > 127 ? __uint_as_float(0x7F800000u) : __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
 // ------------------------------------------------------------------ wave reductions (DPP)

@@ -48,7 +48,11 @@ _SIGS = {
     "tfp8_linear_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "tfp8_linear": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),
     "tfp8_gemv": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P]),
+    "tfp8_gemm_prepared_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "tfp8_gemm_prepared": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "tfp8_tuning_set": (_I, [_c.c_char_p, _I]),
+    "tfp8_tuning_get": (_I, [_c.c_char_p, _P]),
+    "tfp8_tuning_reset": (None, []),
     "tfp8_w8a8_quantize": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "tfp8_w8a8_gemm": (_I, [_P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I, _I, _P]),
 }
@@ -290,13 +294,51 @@ def gemm_prepared(x16, xs, qweight, lut16, wscale, bias, out_dtype, group_size, 
     y = torch.empty(M, N, dtype=out_dtype, device=x16.device)
     if M == 0:
         return y
-    nb = lib.tfp8_linear_workspace_size(_dtype_id(x16.dtype), max(M, GEMV_MAXM + 1), N, K)
+    nb = lib.tfp8_gemm_prepared_workspace_size(_dtype_id(x16.dtype), M, N, K)
     ws_buf = _workspace(x16.device, nb)
     _check(lib.tfp8_gemm_prepared(x16.data_ptr(), _dtype_id(x16.dtype), _ptr(xs), M, K, qweight.data_ptr(), N,
                                   wscale.data_ptr(), scale_kind(wscale), group_size, FMT_ID[fmt], _ptr(bias),
                                   y.data_ptr(), _dtype_id(out_dtype), _ptr(ws_buf), nb, _stream(x16.get_device())),
            "tfp8_gemm_prepared")
     return y
+
+
+# ------------------------------------------------------------------ tuning knobs
+def tuning_set(name: str, value: int) -> None:
+    """Force a kernel-selection knob (TFP8_GEMV_CFG, TFP8_GEMM_SPLITK, ...; include/tfp8_hip.h) for
+    every later call in this process.  Workspace sizes follow the knobs: query them afterwards."""
+    _check(library().tfp8_tuning_set(name.encode(), int(value)), "tfp8_tuning_set")
+
+
+def tuning_get(name: str) -> int:
+    v = _c.c_int(0)
+    _check(library().tfp8_tuning_get(name.encode(), _c.byref(v)), "tfp8_tuning_get")
+    return v.value
+
+
+def tuning_reset() -> None:
+    """Every knob back to its value when the library was loaded."""
+    library().tfp8_tuning_reset()
+
+
+class tuning:
+    """Context manager: `with _ext.tuning(TFP8_GEMM_SPLITK=3, TFP8_GEMM_TILE=13): ...` sets the knobs
+    and restores the previous values on exit."""
+
+    def __init__(self, **knobs):
+        self.knobs = knobs
+        self.saved = {}
+
+    def __enter__(self):
+        for k, v in self.knobs.items():
+            self.saved[k] = tuning_get(k)
+            tuning_set(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            tuning_set(k, v)
+        return False
 
 
 class GemvLaunch:

@@ -16,10 +16,12 @@ SCALE_FORMATS = ("f32", "ue8m0")
 
 
 def pow2_ceil(s: torch.Tensor) -> torch.Tensor:
-    """2^ceil(log2 s), exact: from frexp, not from a rounded log2 (s > 0; inf/NaN pass through)."""
-    m, e = torch.frexp(s)
-    p = torch.where(m == 0.5, s, torch.ldexp(torch.ones_like(s), e))
-    return torch.where(torch.isfinite(s), p, s)
+    """2^ceil(log2 s) through torch's fp32 log2, the formula of tfp8/quantize.py:11-12.
+
+    A value a few ULP above a power of two 2^k can have an fp32 log2 that rounds to exactly k, and
+    then the result is 2^k (below s), not 2^(k+1); the gfx950 kernels reproduce that rounding
+    (ceil_log2_ref in tfp8_common.h), so CPU and GPU give the same scales as the reference."""
+    return torch.exp2(torch.ceil(torch.log2(s)))
 
 
 def ue8m0_encode(s: torch.Tensor) -> torch.Tensor:
@@ -96,13 +98,7 @@ def activation_to_fp16(x: torch.Tensor):
     if x.is_cuda:
         return _ext.prepare_activations(x)
     amax = x.abs().amax(-1).float()
-    e = _ceil_log2(amax.clamp_min(2.0 ** -100)) - ACT_TARGET_EXP
+    e = torch.ceil(torch.log2(amax.clamp_min(2.0 ** -100))) - ACT_TARGET_EXP   # quantize.py:58-60
     e = torch.where(amax > 0, e, torch.zeros_like(e))
-    xs = torch.ldexp(torch.ones_like(amax), e)
+    xs = torch.exp2(e)
     return (x.float() / xs[:, None]).half().contiguous(), xs.contiguous()
-
-
-def _ceil_log2(a: torch.Tensor) -> torch.Tensor:
-    """ceil(log2 a) for a > 0, exact from frexp."""
-    m, e = torch.frexp(a)
-    return torch.where(m == 0.5, e - 1, e)

@@ -126,13 +126,31 @@ int tfp8_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
 /*
  * The MFMA GEMM alone on f16 or bf16 activations, with an optional per-row f32 scale xs [M]
  * (NULL = 1), i.e. _ext.gemm_prepared (tfp8/_ext.py:267-275) / gemm_w8a16
- * (tfp8/csrc/tfp8_kernels.cu:296-411).  Any M >= 1.  Workspace as for tfp8_linear with
- * x_dtype = x16_dtype.
+ * (tfp8/csrc/tfp8_kernels.cu:296-411).  Any M >= 1 (M <= 8 runs the GEMM kernels too, not the
+ * GEMV).  The workspace (split-K partial sums) must hold tfp8_gemm_prepared_workspace_size(M, N, K)
+ * bytes, 256-byte aligned; that size can be non-zero for every M, including M <= 8.
  */
+size_t tfp8_gemm_prepared_workspace_size(int x16_dtype, int M, int N, int K);
 int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, int K,
                        const uint8_t* w, int N, const void* ws, int ws_kind, int G, int fmt,
                        const float* bias, void* y, int y_dtype, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- tuning knobs
+ * No counterpart in the reference (its kernels are resolved once per device, tfp8/_ext.py:67-76).
+ * Kernel-selection overrides for sweeps and for tests that force every compiled configuration:
+ * TFP8_GEMV_CFG, TFP8_GEMV_WPC, TFP8_GEMV_MFMA_MIN, TFP8_GEMV_MFMA_MAX_M, TFP8_GM_NT, TFP8_GM_W,
+ * TFP8_GM_D, TFP8_GM_TL, TFP8_GEMM_TILE, TFP8_GEMM_SPLITK, TFP8_GEMM_DIRECT, TFP8_GEMM_DIRECT_MIN_M,
+ * TFP8_GEMM_DCFG, TFP8_GS_NW, TFP8_GS_KCS, TFP8_GS_SPLITK, TFP8_GS_TL, TFP8_GEMM_V1.  Each starts at
+ * the value of the environment variable of that name when the library is loaded (or its default),
+ * and changes only through tfp8_tuning_set; the launch path never reads the environment.  A knob
+ * changes routing and workspace sizes for every later call in the process: size workspaces after
+ * setting knobs.  tfp8_tuning_reset restores the values read at load.  Unknown names give
+ * TFP8_ERR_ARG.
+ */
+int tfp8_tuning_set(const char* name, int value);
+int tfp8_tuning_get(const char* name, int* value);
+void tfp8_tuning_reset(void);
 
 /* ---------------------------------------------------------------- W8A8, 32-wide K-block scales
  * FP8 activations x FP8 weights (reference fp8_cuda.py / fp8_gemm_kernel.cu).

@@ -92,12 +92,33 @@ def encode(x, fmt):
     return q.astype(np.uint8).reshape(xd.shape)
 
 
-def pow2_ceil(s):
-    """2^ceil(log2 s) for s > 0 (tfp8/quantize.py:11-12), computed exactly from frexp."""
+def ceil_log2_f32(s):
+    """ceil(log2 s) of the reference's fp32 formula (tfp8/quantize.py:11-12 and :58-59): the
+    log2 of an fp32 value rounded once to fp32, then the ceiling.  Computed as float64 log2
+    rounded to float32, i.e. the correctly rounded fp32 log2 (float64 carries 29 bits more than
+    that rounding needs).  A value a few ULP above 2^k has an fp32 log2 of exactly k, so its
+    ceiling is k, not k + 1."""
+    s = np.asarray(s, dtype=np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.ceil(np.log2(s.astype(np.float64)).astype(np.float32))
+
+
+def pow2_ceil_exact(s):
+    """2^ceil(log2 s) from the exponent bits (no rounded log2): the power of two at or above s."""
     s = np.asarray(s, dtype=np.float32)
     m, e = np.frexp(s)
     p = np.where(m == 0.5, s, np.ldexp(np.float32(1.0), e).astype(np.float32))
     return np.where(np.isfinite(s), p, s).astype(np.float32)
+
+
+def pow2_ceil(s):
+    """torch.exp2(torch.ceil(torch.log2(s))) (tfp8/quantize.py:11-12) for s > 0; inf and NaN pass
+    through.  Equals pow2_ceil_exact except a few ULP above a power of two (ceil_log2_f32)."""
+    s = np.asarray(s, dtype=np.float32)
+    c = ceil_log2_f32(s)
+    fin = np.isfinite(c)
+    p = np.ldexp(np.float32(1.0), np.where(fin, c, 0).astype(np.int32)).astype(np.float32)
+    return np.where(fin, p, s).astype(np.float32)
 
 
 def ue8m0_encode(s):
@@ -157,14 +178,13 @@ ACT_TARGET_EXP = 8
 
 
 def activation_to_fp16(x):
-    """(x16 fp16, xs f32 pow2) per row: e = ceil(log2 max(amax, 2^-100)) - 8, 0 for amax == 0
-    (tfp8/quantize.py:47-62; the kernel variant tfp8_kernels.cu:513-532 rescales fp16 input too)."""
+    """(x16 fp16, xs f32 pow2) per row: e = ceil(log2 max(amax, 2^-100)) - 8 with the fp32 log2
+    rounding of ceil_log2_f32, 0 for amax == 0 (tfp8/quantize.py:47-62; the kernel variant
+    tfp8_kernels.cu:513-532 rescales fp16 input too)."""
     x = np.asarray(x, dtype=np.float32)
     amax = np.abs(x).max(-1)
-    a = np.maximum(amax, np.float32(2.0 ** -100))
-    m, e = np.frexp(a)
-    cl = np.where(m == 0.5, e - 1, e)
-    ex = np.where(amax > 0, cl - ACT_TARGET_EXP, 0).astype(np.int32)
+    cl = ceil_log2_f32(np.maximum(amax, np.float32(2.0 ** -100)))
+    ex = np.where(amax > 0, np.nan_to_num(cl) - ACT_TARGET_EXP, 0).astype(np.int32)
     xs = np.ldexp(np.float32(1.0), ex).astype(np.float32)
     return (x / xs[:, None]).astype(np.float16), xs
 

@@ -22,3 +22,16 @@ def pytest_collection_modifyitems(config, items):
     for it in items:
         if "gpu" in it.keywords:
             it.add_marker(skip)
+
+
+@pytest.fixture
+def tune():
+    """Sets libtfp8_hip.so tuning knobs for one test (tune(TFP8_GEMM_SPLITK=3, ...)); every knob is
+    back at its load-time value afterwards."""
+    from tfp8 import _ext
+
+    def set_knobs(**knobs):
+        for k, v in knobs.items():
+            _ext.tuning_set(k, int(v))
+    yield set_knobs
+    _ext.tuning_reset()

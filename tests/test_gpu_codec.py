@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 import torch
 
+import binade_edges
 from oracle import fp8_oracle as O
 from tfp8 import _ext
 from tfp8.formats import E4M3FN, E5M2, decode, encode, lut
@@ -112,6 +113,32 @@ def test_quantize_weight_nan_group():
     assert _same(s.cpu(), torch.from_numpy(os_))
     ok = ~torch.isnan(torch.from_numpy(os_)).repeat_interleave(32, dim=1)
     assert torch.equal(q.cpu()[ok], torch.from_numpy(oq)[ok])
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("sf", ["f32", "ue8m0"])
+def test_quantize_weight_binade_edges(fmt, sf):
+    """Group scales a few ULP above a power of two: the kernel's power-of-two ceiling follows the
+    reference's fp32 log2 rounding (tfp8/quantize.py:11-12), codes and scales bit-exact against
+    the oracle, with hundreds of groups inside the rounding window."""
+    print(f"[quantize binade edges] fmt={fmt} sf={sf}", flush=True)
+    w = binade_edges.weight_rows(fmt)
+    assert binade_edges.window_hits(w, fmt, 32) > 500
+    q, s, G = quantize_weight(torch.from_numpy(w).cuda(), fmt, 32, True, sf)
+    oq, os_, _ = O.quantize_weight(w, fmt, 32, True, sf)
+    assert torch.equal(s.cpu(), torch.from_numpy(os_))
+    assert torch.equal(q.cpu(), torch.from_numpy(oq))
+
+
+def test_prepare_activations_binade_edges():
+    """fp32 rows whose amax is 2^k (1 + j 2^-23): the row exponent follows the reference's fp32
+    log2 rounding (tfp8/quantize.py:58-60), bit-exact against the oracle."""
+    print("[prep binade edges]", flush=True)
+    x = binade_edges.activation_rows()
+    x16, xs = _ext.prepare_activations(torch.from_numpy(x).cuda())
+    ox16, oxs = O.activation_to_fp16(x)
+    assert torch.equal(xs.cpu(), torch.from_numpy(oxs))
+    assert torch.equal(x16.cpu().view(torch.int16), torch.from_numpy(ox16.view(np.int16)))
 
 
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32, torch.float16])

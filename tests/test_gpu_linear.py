@@ -8,7 +8,6 @@ dtypes, pipeline edges, folded group scales, empty / non-contiguous / N-d input,
 launch state, NaN fallback) and every benchmark configuration (C1-C4) at its full size, plus the reference's
 CPU dequantize-then-matmul path as a second reference.
 """
-import os
 
 import numpy as np
 import pytest
@@ -172,7 +171,7 @@ def test_gemv_prepared_launch_tracks_layer_state():
             y = f(x)
             assert torch.equal(y, general(x)), (xd, M)
             _check(y, x, f.qweight, f.weight_scale, 128, "e4m3fn", f.bias_f32, f.out_dtype, "gemv", f"{xd} M={M}")
-    assert len(f._gemv) == 3
+    assert len(f._bindings) == 3
     x = torch.randn(2, 3, 512, device="cuda", dtype=torch.bfloat16)
     assert torch.equal(f(x), general(x).reshape(2, 3, 200))
     x = torch.randn(4, 512, device="cuda", dtype=torch.bfloat16)
@@ -315,29 +314,29 @@ def test_config4_e5m2_block32_ue8m0():
 
 
 @pytest.mark.parametrize("tile", list(range(1, 14)))
-def test_tiled_gemm_every_config(tile, monkeypatch):
+def test_tiled_gemm_every_config(tile, tune):
     """Every LDS-tiled GEMM configuration (forced through the library's tuning hooks), with and
     without split-K, on ragged shapes: rows past M and N, a K tail that is not a whole K tile,
     per-channel and K-group (f32 G=32, UE8M0 G=64) scales, f16 and bf16 activations."""
-    monkeypatch.setenv("TFP8_GEMM_V1", "1")
-    monkeypatch.setenv("TFP8_GEMM_DIRECT", "0")
-    monkeypatch.setenv("TFP8_GEMM_TILE", str(tile))
+    tune(TFP8_GEMM_V1=1)
+    tune(TFP8_GEMM_DIRECT=0)
+    tune(TFP8_GEMM_TILE=tile)
     for split in (1, 3):
-        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+        tune(TFP8_GEMM_SPLITK=split)
         _run(40, 200, 1120, None, torch.float16, xdt=torch.float16, seed=tile)
         _run(130, 72, 640, 32, torch.bfloat16, xdt=torch.bfloat16, seed=tile + 1)
         _run(257, 136, 704, 64, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", seed=tile + 2)
 
 
-@pytest.mark.parametrize("direct", ["0", "1"])
-def test_split_k_workspace_contents_do_not_matter(direct, monkeypatch):
+@pytest.mark.parametrize("direct", [0, 1])
+def test_split_k_workspace_contents_do_not_matter(direct, tune):
     """Split-K through the caller's workspace (fp32 partial tiles, then the reduce kernel): a
     workspace full of garbage, or one reused from the previous call, gives the same bits every
     time, within the oracle tolerance (LDS-tiled kernel and direct-load kernel)."""
-    monkeypatch.setenv("TFP8_GEMM_V1", "1")
-    monkeypatch.setenv("TFP8_GEMM_DIRECT", direct)
-    monkeypatch.setenv("TFP8_GEMM_TILE", "13")
-    monkeypatch.setenv("TFP8_GEMM_SPLITK", "3")
+    tune(TFP8_GEMM_V1=1)
+    tune(TFP8_GEMM_DIRECT=direct)
+    tune(TFP8_GEMM_TILE=13)
+    tune(TFP8_GEMM_SPLITK=3)
     lib = _ext.require()
     M, N, K = 200, 512, 3072
     q, s, G, b = _layer(N, K, None, "e4m3fn", "ue8m0", seed=21)
@@ -370,12 +369,12 @@ def test_split_k_workspace_contents_do_not_matter(direct, monkeypatch):
     (1000, 2048, 1024, torch.float16, torch.float16, "e5m2", "ue8m0", True, 1),
     (300, 512, 512, torch.float32, torch.float32, "e4m3fn", "f32", True, 2),      # fp32 x: f16 prep + row scales
 ])
-def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, monkeypatch):
+def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, tune):
     """The direct-load GEMM (M > 128, one scale per weight row): rows past M and N inside a tile,
     K of one to three steps (fewer than the LDS ring holds), even and uneven split-K, f16 / bf16 /
     fp32 activations, both formats, f32 and UE8M0 scales, every output dtype."""
     if split:
-        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+        tune(TFP8_GEMM_SPLITK=split)
     _run(M, N, K, None, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=M + K)
 
 
@@ -387,37 +386,37 @@ def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, monkeypatch
     (130, 256, 4096, 128, "f32", torch.bfloat16, "e4m3fn", 0),     # split 8, slices of 4 groups
     (150, 640, 2304, 192, "f32", torch.bfloat16, "e5m2", 5),       # slices of 512 cut groups of 192
 ])
-def test_direct_gemm_group_scales(M, N, K, G, sf, xdt, fmt, split, monkeypatch):
+def test_direct_gemm_group_scales(M, N, K, G, sf, xdt, fmt, split, tune):
     """K-group scales on the direct-load GEMM: UE8M0 groups folded into the decode (bf16
     activations), and f32 / UE8M0 groups with G % 64 == 0 applied to an fp32 partial sum at each
     group boundary, including split-K slices that start inside a group."""
     if split:
-        monkeypatch.setenv("TFP8_GEMM_SPLITK", str(split))
+        tune(TFP8_GEMM_SPLITK=split)
     _run(M, N, K, G, torch.float32, fmt=fmt, xdt=xdt, sf=sf, seed=M + G)
 
 
 @pytest.mark.parametrize("cfg", list(range(1, 8)))
-def test_direct_gemm_every_config(cfg, monkeypatch):
+def test_direct_gemm_every_config(cfg, tune):
     """Every direct-load GEMM configuration (block tile 32/64/128 x 128/256, 4 or 8 waves, rings of
     3 to 7 K steps), forced through the library's tuning hooks at small and large M: rows past M
     inside a tile, several row tiles, columns past N, one-step and long K slices."""
-    monkeypatch.setenv("TFP8_GEMM_DIRECT_MIN_M", "9")
-    monkeypatch.setenv("TFP8_GEMM_DCFG", str(cfg))
+    tune(TFP8_GEMM_DIRECT_MIN_M=9)
+    tune(TFP8_GEMM_DCFG=cfg)
     _run(20, 520, 64, None, torch.float16, xdt=torch.float16, sf="ue8m0", seed=cfg)
     _run(100, 392, 1088, None, torch.bfloat16, fmt="e5m2", xdt=torch.bfloat16, seed=cfg + 1)
     _run(300, 1024, 3072, None, torch.float32, xdt=torch.float16, seed=cfg + 2)
 
 
 @pytest.mark.parametrize("nt,w,d", [(2, 8, 4), (2, 8, 8), (2, 4, 4), (2, 4, 8), (1, 8, 4), (1, 8, 8), (1, 4, 4), (1, 4, 8)])
-def test_decode_mfma_every_config(nt, w, d, monkeypatch):
+def test_decode_mfma_every_config(nt, w, d, tune):
     """The matrix-core decode kernel (up to 16 rows) in every compiled configuration, forced down to
     M = 1: rows past N in the last block, a K tail that is not a whole 64-byte chunk, K ranges that
     leave some waves without work, per-channel / f32 K-group (G=64) / UE8M0 K-group (G=32) scales,
     both formats, f16 and bf16 activations, with and without bias."""
-    monkeypatch.setenv("TFP8_GEMV_MFMA_MIN", "1")
-    monkeypatch.setenv("TFP8_GM_NT", str(nt))
-    monkeypatch.setenv("TFP8_GM_W", str(w))
-    monkeypatch.setenv("TFP8_GM_D", str(d))
+    tune(TFP8_GEMV_MFMA_MIN=1)
+    tune(TFP8_GM_NT=nt)
+    tune(TFP8_GM_W=w)
+    tune(TFP8_GM_D=d)
     _run(1, 72, 720, None, torch.bfloat16, xdt=torch.bfloat16, seed=nt * 100 + w * 10 + d)   # K tail 16
     _run(5, 200, 1152, 64, torch.float16, xdt=torch.float16, seed=nt + w + d)
     _run(8, 136, 544, 32, torch.float32, fmt="e5m2", xdt=torch.bfloat16, sf="ue8m0", bias=False, seed=d)  # tail 32
@@ -432,17 +431,17 @@ def test_decode_mfma_every_config(nt, w, d, monkeypatch):
 
 @pytest.mark.parametrize("M,N,K,G,sf", [(16, 8192, 8192, None, "ue8m0"), (24, 1000, 2048, 128, "f32"),
                                         (32, 520, 4096, 32, "ue8m0"), (13, 300, 832, 64, "f32")])
-def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
+def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, tune):
     """The weight-streaming GEMM's transposed weight loads (256-code chunks as 4 rows x 256 bytes,
     regrouped through LDS) against its direct operand-layout loads: bit-identical outputs (same
     operands, same order), including the K tail, rows past N and split-K."""
     print(f"[linear] stream transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
-    monkeypatch.setenv("TFP8_GEMV_MFMA_MAX_M", "8")   # M <= 16 would take the matrix-core decode kernel
+    tune(TFP8_GEMV_MFMA_MAX_M=8)   # M <= 16 would take the matrix-core decode kernel
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().cuda()
     outs = []
-    for tl in ("0", "1"):
-        monkeypatch.setenv("TFP8_GS_TL", tl)
+    for tl in (0, 1):
+        tune(TFP8_GS_TL=tl)
         outs.append(_ext.w8a16(x, q, None, s, b, torch.float16, GG, "e4m3fn"))
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
@@ -452,7 +451,7 @@ def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
 @pytest.mark.parametrize("M,N,K,G,sf", [(4, 14336, 4096, 128, "f32"), (8, 4096, 4096, None, "ue8m0"),
                                         (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32"),
                                         (16, 8192, 8192, None, "ue8m0"), (12, 14336, 4096, 128, "f32")])
-def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
+def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, tune):
     """The decode kernel's transposed weight loads (4 rows x 256 bytes per load, regrouped through
     LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
     64 bytes per load): the outputs must be bit-identical."""
@@ -460,8 +459,8 @@ def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, monkeypatch):
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).bfloat16().cuda()
     outs = []
-    for tl in ("0", "1"):
-        monkeypatch.setenv("TFP8_GM_TL", tl)
+    for tl in (0, 1):
+        tune(TFP8_GM_TL=tl)
         outs.append(_ext.w8a16(x, q, None, s, b, torch.bfloat16, GG, "e4m3fn"))
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
@@ -486,13 +485,10 @@ def test_weight_matrix_past_2gib():
     torch.cuda.empty_cache()
     cols = np.r_[0:48, N - 80:N]
     qs, ss = q[cols].cpu().numpy(), s[cols].cpu().numpy()
-    for M, mfma_max in ((1, "16"), (4, "16"), (16, "16"), (16, "8"), (128, "16")):
-        os.environ["TFP8_GEMV_MFMA_MAX_M"] = mfma_max
+    for M, mfma_max in ((1, 16), (4, 16), (16, 16), (16, 8), (128, 16)):
         x = (torch.randn(M, K, generator=g, device="cuda") * 0.5).bfloat16()
-        try:
+        with _ext.tuning(TFP8_GEMV_MFMA_MAX_M=mfma_max):
             y = _ext.w8a16(x, q, None, s, None, torch.float32, G, "e4m3fn")
-        finally:
-            os.environ.pop("TFP8_GEMV_MFMA_MAX_M")
         ref = O.linear_ref64(_x_eff(x, "gemv" if M <= _ext.GEMV_MAXM else "gemm"), qs, ss, G, "e4m3fn", None)
         got = y[:, cols].double().cpu().numpy()
         d = np.abs(got - ref)

@@ -10,6 +10,7 @@ import pytest
 import torch
 import torch.nn as nn
 
+import binade_edges
 import tfp8
 from oracle import fp8_oracle as O
 from tfp8 import _ext
@@ -71,6 +72,26 @@ def test_cpu_quantize_nonpow2_matches_oracle():
     q, s, G = quantize_weight(w, "e4m3fn", 32, False)
     oq, os_, _ = O.quantize_weight(w.numpy(), "e4m3fn", 32, False)
     assert torch.equal(q, torch.from_numpy(oq)) and torch.equal(s, torch.from_numpy(os_))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+@pytest.mark.parametrize("sf", ["f32", "ue8m0"])
+def test_cpu_quantize_binade_edges_match_oracle(fmt, sf):
+    """Scales a few ULP above a power of two round as the reference's fp32 log2 does
+    (tfp8/quantize.py:11-12) on the CPU path too."""
+    w = binade_edges.weight_rows(fmt)
+    assert binade_edges.window_hits(w, fmt, 32) > 500
+    q, s, G = quantize_weight(torch.from_numpy(w), fmt, 32, True, sf)
+    oq, os_, _ = O.quantize_weight(w, fmt, 32, True, sf)
+    assert torch.equal(s, torch.from_numpy(os_)) and torch.equal(q, torch.from_numpy(oq))
+
+
+def test_cpu_activation_prep_binade_edges_match_oracle():
+    x = binade_edges.activation_rows()
+    x16, xs = activation_to_fp16(torch.from_numpy(x))
+    ox16, oxs = O.activation_to_fp16(x)
+    assert torch.equal(xs, torch.from_numpy(oxs))
+    assert torch.equal(x16.view(torch.int16), torch.from_numpy(ox16.view(np.int16)))
 
 
 def test_activation_scaling_is_exact_power_of_two():
@@ -204,7 +225,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     names = _header_functions()
-    assert len(names) == 13, names
+    assert len(names) == 17, names
     lib = ctypes.CDLL(_ext.lib_path())
     for n in names:
         assert hasattr(lib, n), n
@@ -225,6 +246,8 @@ def _header_prototypes():
 
 
 def _ctypes_kind(ctype):
+    if ctype == "void":
+        return None
     if "*" in ctype:
         return ctypes.c_char_p if ctype.replace(" ", "") == "constchar*" else ctypes.c_void_p
     return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
@@ -242,6 +265,43 @@ def test_bound_argument_kinds_match_header():
         res, args = _ext._SIGS[name]
         assert args == [_ctypes_kind(t) for t in params], (name, params)
         assert res == _ctypes_kind(ret), (name, ret)
+
+
+def test_gemm_prepared_workspace_query_covers_small_m():
+    """tfp8_gemm_prepared runs the GEMM kernels at every M, so its workspace query is non-zero
+    wherever they split K -- also for M <= 8, where tfp8_linear (GEMV) needs none."""
+    lib = _ext.library()
+    for M in range(1, 9):
+        assert lib.tfp8_linear_workspace_size(0, M, 4096, 4096) == 0
+        nb = lib.tfp8_gemm_prepared_workspace_size(0, M, 4096, 4096)
+        assert nb >= lib.tfp8_gemm_prepared_workspace_size(0, M, 64, 64)
+    assert lib.tfp8_gemm_prepared_workspace_size(0, 1, 8192, 8192) >= 0
+    assert lib.tfp8_gemm_prepared_workspace_size(0, 256, 8192, 8192) == lib.tfp8_linear_workspace_size(0, 256, 8192, 8192)
+    assert lib.tfp8_gemm_prepared_workspace_size(0, 0, 64, 64) == 0
+
+
+def test_tuning_knobs_set_get_reset():
+    """Knobs change only through the setter (the launch path never reads the environment), unknown
+    names are argument errors, reset restores the load-time values, and a knob that forces split-K
+    changes the workspace size the library asks for."""
+    lib = _ext.library()
+    base = _ext.tuning_get("TFP8_GEMM_SPLITK")
+    ws0 = lib.tfp8_linear_workspace_size(0, 200, 512, 3072)
+    with _ext.tuning(TFP8_GEMM_SPLITK=3, TFP8_GEMM_DIRECT=0):
+        assert _ext.tuning_get("TFP8_GEMM_SPLITK") == 3 and _ext.tuning_get("TFP8_GEMM_DIRECT") == 0
+        ws3 = lib.tfp8_linear_workspace_size(0, 200, 512, 3072)
+    assert _ext.tuning_get("TFP8_GEMM_SPLITK") == base and _ext.tuning_get("TFP8_GEMM_DIRECT") == 1
+    assert ws3 != ws0 or ws0 == 0
+    os.environ["TFP8_GEMM_SPLITK"] = "5"                  # read at load only: no effect now
+    try:
+        assert _ext.tuning_get("TFP8_GEMM_SPLITK") == base
+    finally:
+        os.environ.pop("TFP8_GEMM_SPLITK")
+    assert lib.tfp8_tuning_set(b"TFP8_NO_SUCH_KNOB", 1) == -1
+    assert "unknown knob" in lib.tfp8_last_error().decode()
+    _ext.tuning_set("TFP8_GEMV_CFG", 8)
+    _ext.tuning_reset()
+    assert _ext.tuning_get("TFP8_GEMV_CFG") == -1
 
 
 def test_abi_argument_validation_without_gpu():

@@ -5,7 +5,8 @@ Each oracle function is tied to something independent of its own code:
                           casts, and the special values of the reference test (test_tfp8.py:37-45)
   encode                  torch's RNE float8 cast on in-range values (test_tfp8.py:48-53), an
                           exhaustive nearest-code scan at every midpoint, saturation and NaN codes
-  pow2_ceil / ue8m0_*     closed forms with Python's exact float arithmetic
+  pow2_ceil / ue8m0_*     closed forms: the fp32-log2 rounding window above each power of two
+                          (from log2(1+f) = f/ln2), torch's own log2, exact powers of two
   quantize_weight         the reference's torch formula (quantize.py:15-36) run with torch ops
   dequantize_weight       exact float64 products (pow2) / one f32 rounding (non-pow2)
   activation_to_fp16      exactness invariant (test_tfp8.py:58-62) and the torch formula
@@ -111,20 +112,52 @@ def test_encode_round_trips_every_finite_code(fmt):
     assert int(fin.sum()) == (254 if fmt == "e4m3fn" else 248)
 
 
+def _jmax(k):
+    """Closed form of the fp32-log2 rounding: for s = 2^k (1 + j 2^-23), log2 s rounds to exactly
+    k (so ceil(log2 s) = k) iff 0 < j <= floor(ln2 * 2^p), where 2^(p - 22) is the gap from k to
+    the next fp32 value toward +inf (half of 2^(floor(log2|k|) - 23) below a negative power of
+    two).  Derived from log2(1 + f) = f / ln2 + O(f^2), not from any log2 implementation."""
+    if k == 0:
+        return 0
+    fl = int(math.floor(math.log2(abs(k))))
+    if k < 0 and (abs(k) & (abs(k) - 1)) == 0:
+        fl -= 1
+    return int(math.floor(math.log(2.0) * 2.0 ** (fl - 1)))
+
+
+def _edge_grid(jmax=80):
+    k = np.arange(-126, 128)
+    j = np.arange(0, jmax + 1)
+    kk, jj = np.meshgrid(k, j, indexing="ij")
+    s = np.ldexp(1.0 + jj * 2.0 ** -23, kk).astype(np.float32)
+    assert np.array_equal(s.astype(np.float64), np.ldexp(1.0 + jj * 2.0 ** -23, kk))   # exact
+    return kk, jj, s
+
+
 def test_pow2_ceil_closed_form():
+    # every exponent, the 80 values above each power of two: the closed form of the rounding
+    kk, jj, s = _edge_grid()
+    want = np.where((jj == 0) | (jj <= np.vectorize(_jmax)(kk)), kk, kk + 1)
+    assert np.array_equal(O.ceil_log2_f32(s), want.astype(np.float32))
+    assert np.array_equal(O.pow2_ceil(s), np.ldexp(np.float32(1.0), want).astype(np.float32))
+    assert int((want == kk)[jj > 0].sum()) > 3000      # the window is not empty
+    # torch's own fp32 log2 (an independent implementation) agrees with it everywhere here
+    ts = torch.from_numpy(s)
+    assert np.array_equal(torch.exp2(torch.ceil(torch.log2(ts))).numpy(), O.pow2_ceil(s))
+    # away from the window: the exact power of two at or above s
     rng = np.random.default_rng(1)
-    s = (rng.random(2000) * 10.0 ** rng.integers(-30, 30, 2000)).astype(np.float32)
-    s = s[s > 0]
-    got = O.pow2_ceil(s)
-    for a, g in zip(s.tolist(), got.tolist()):
+    r = (rng.random(2000) * 10.0 ** rng.integers(-30, 30, 2000)).astype(np.float32)
+    r = r[(r > 0) & ((r.view(np.uint32) & 0x7FFFFF) > 64)]
+    got = O.pow2_ceil(r)
+    for a, g in zip(r.tolist(), got.tolist()):
         m, e = math.frexp(a)
-        want = a if m == 0.5 else math.ldexp(1.0, e)
-        assert g == want
-    # one ulp above a power of two rounds up, exact powers stay
+        assert g == math.ldexp(1.0, e)
+    assert np.array_equal(got, O.pow2_ceil_exact(r))
     for k in (-126, -20, -7, -4, 0, 3, 60):
         p = np.float32(math.ldexp(1.0, k))
-        assert O.pow2_ceil(p) == p
-        assert O.pow2_ceil(np.nextafter(p, np.float32(np.inf))) == np.float32(math.ldexp(1.0, k + 1))
+        assert O.pow2_ceil(p) == p == O.pow2_ceil_exact(p)
+    # a planted mistake -- the exact ceiling -- differs from the reference rounding in the window
+    assert not np.array_equal(O.pow2_ceil_exact(s), O.pow2_ceil(s))
 
 
 def test_ue8m0_closed_form():
@@ -197,12 +230,23 @@ def test_activation_to_fp16_exact_and_matches_torch_formula():
     x16, xs = O.activation_to_fp16(x.float().numpy())
     assert np.all(np.log2(xs) == np.round(np.log2(xs)))
     assert np.array_equal(x16.astype(np.float32) * xs[:, None], x.float().numpy())
-    # reference formula (log2-based) agrees away from exact powers of two
+    # reference formula (log2-based)
     amax = x.float().abs().amax(-1)
     e = torch.ceil(torch.log2(amax)) - 8
     assert np.array_equal(torch.exp2(e).numpy(), xs)
     zero = O.activation_to_fp16(np.zeros((1, 8), np.float32))[1]
     assert zero[0] == 1.0
+    # fp32 rows whose amax sits a few ULP above a power of two: e follows the fp32 log2 rounding
+    kk, jj, s = _edge_grid(24)
+    rows = np.zeros((s.size, 16), np.float32)
+    rows[:, 3] = -s.reshape(-1)
+    rows[:, 7] = s.reshape(-1) * np.float32(0.25)
+    ok = s.reshape(-1) >= 2.0 ** -100
+    x16, xs = O.activation_to_fp16(rows[ok])
+    want = torch.exp2(torch.ceil(torch.log2(torch.from_numpy(s.reshape(-1)[ok]))) - 8).numpy()
+    assert np.array_equal(xs, want)
+    exact = np.ldexp(np.float32(1.0), np.ceil(np.log2(s.reshape(-1)[ok].astype(np.float64))).astype(np.int32) - 8)
+    assert not np.array_equal(xs, exact.astype(np.float32))   # the window is hit
 
 
 def test_linear_ref64_bruteforce_and_torch():
