@@ -2,6 +2,9 @@
 // above, as tfp8/_ext.py:230-253 routes), workspace layout.
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "tfp8_common.h"
 
 namespace tfp8 {
@@ -85,6 +88,10 @@ extern "C" int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* x
                     (hipStream_t)stream);
 }
 
+// The body of tfp8_linear after validation, on a workspace already checked to be large enough.
+static int linear_run(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
+                      int G, int fmt, const float* bias, void* y, int y_dtype, void* workspace, void* stream);
+
 extern "C" int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws,
                            int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, void* workspace,
                            size_t workspace_bytes, void* stream) {
@@ -93,13 +100,17 @@ extern "C" int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8
     if (int rc = check_linear("tfp8_linear", x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, y, y_dtype, gemm))
         return rc;
     if (M == 0 || N == 0) return 0;
-    hipStream_t s = (hipStream_t)stream;
-    if (!gemm) return run_gemv(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
-
-    const size_t need = tfp8_linear_workspace_size(x_dtype, M, N, K);
+    const size_t need = gemm ? tfp8_linear_workspace_size(x_dtype, M, N, K) : 0;
     if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
         return fail(TFP8_ERR_WORKSPACE, "tfp8_linear: need %zu bytes of 256-aligned workspace, got %zu", need,
                     workspace ? workspace_bytes : (size_t)0);
+    return linear_run(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, workspace, stream);
+}
+
+static int linear_run(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
+                      int G, int fmt, const float* bias, void* y, int y_dtype, void* workspace, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (M <= GEMV_MAXM) return run_gemv(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
     uint8_t* wsp = (uint8_t*)workspace;
     if (x_dtype == TFP8_F32) {
         // fp32 activations: fp16 with an exact power-of-two row scale (tfp8/quantize.py:47-62).
@@ -110,4 +121,70 @@ extern "C" int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8
         return run_gemm(x16, TFP8_F16, xs, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, part, s);
     }
     return run_gemm(x, x_dtype, nullptr, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, (float*)wsp, s);
+}
+
+// ------------------------------------------------------------------ no-allocation entry point
+// tfp8_linear for callers that cannot allocate (code under HIP graph capture, serving loops,
+// harnesses that forbid hipMalloc): the workspace is this file-scope device array instead of a
+// caller buffer.  Each GPU holds its own copy, at its own address, from module load until the
+// process ends.  Host code never passes `scratch` itself (in host code the name is a stand-in,
+// not a device address): its address on each device comes from hipGetSymbolAddress, once per
+// device, with that device current, and only that pointer is used.
+namespace tfp8 {
+
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;   // TFP8_NOALLOC_SCRATCH_BYTES in the header
+static_assert(NOALLOC_SCRATCH_BYTES == TFP8_NOALLOC_SCRATCH_BYTES, "header and library agree on the limit");
+
+__device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static std::atomic<void*> g_scratch[SCRATCH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch`, resolved on the first call made with that device current.
+static int scratch_for_current_device(void** out) {
+    int dev = -1;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) return fail((int)ge, "tfp8_linear_noalloc: hipGetDevice failed: %s", hipGetErrorString(ge));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+        return fail(TFP8_ERR_ARG, "tfp8_linear_noalloc: device %d out of range", dev);
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(e != hipSuccess ? (int)e : TFP8_ERR_ARG,
+                            "tfp8_linear_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                            hipGetErrorString(e));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return 0;
+}
+
+}  // namespace tfp8
+
+extern "C" int tfp8_linear_noalloc(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws,
+                                   int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype,
+                                   void* stream) {
+    clear_error();
+    const bool gemm = M > GEMV_MAXM;
+    if (int rc = check_linear("tfp8_linear_noalloc", x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, y, y_dtype, gemm))
+        return rc;
+    if (M == 0 || N == 0) return 0;
+    const size_t need = gemm ? tfp8_linear_workspace_size(x_dtype, M, N, K) : 0;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(TFP8_ERR_WORKSPACE,
+                    "tfp8_linear_noalloc: M=%d N=%d K=%d needs %zu bytes of workspace, more than the %zu-byte "
+                    "scratch; use tfp8_linear with a caller workspace",
+                    M, N, K, need, NOALLOC_SCRATCH_BYTES);
+    void* sp = nullptr;
+    if (need)
+        if (int rc = scratch_for_current_device(&sp)) return rc;
+    // Nothing in the scratch needs clearing: split-K slices overwrite every partial they own and
+    // the fp32-activation prep writes every fp16 value and row scale before they are read.
+    return linear_run(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, sp, stream);
 }

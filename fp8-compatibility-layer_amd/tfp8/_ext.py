@@ -47,6 +47,7 @@ _SIGS = {
     "tfp8_dequant": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _I, _P]),
     "tfp8_linear_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "tfp8_linear": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "tfp8_linear_noalloc": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P]),
     "tfp8_gemv": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P]),
     "tfp8_gemm_prepared_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "tfp8_gemm_prepared": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _SZ, _P]),

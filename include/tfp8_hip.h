@@ -118,6 +118,23 @@ int tfp8_linear(const void* x, int x_dtype, int M, int K, const uint8_t* w, int 
                 const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
                 int y_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * tfp8_linear without a caller workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  Same arguments, routing, kernels and results as tfp8_linear; its split-K
+ * partial sums and fp32-activation staging go to a library-owned scratch array of
+ * TFP8_NOALLOC_SCRATCH_BYTES per GPU (held from library load until the process ends), so it calls
+ * no hipMalloc/hipFree.  A shape whose tfp8_linear_workspace_size() exceeds that returns
+ * TFP8_ERR_WORKSPACE without launching.  All calls on one GPU share its scratch: calls that
+ * overlap on one GPU (several streams or host threads at once) race and must be serialised by the
+ * caller; calls in order on one stream are safe.  The first call with a device current resolves
+ * that device's scratch address (hipGetSymbolAddress) -- make that call outside graph capture.
+ */
+#define TFP8_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tfp8_linear_noalloc(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
+                        const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
+                        int y_dtype, void* stream);
+
 /* The GEMV alone (1 <= M <= 8), any x_dtype; GEMV kernels of tfp8/csrc/tfp8_kernels.cu:171-269. */
 int tfp8_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N,
               const void* ws, int ws_kind, int G, int fmt, const float* bias, void* y,
