@@ -5,15 +5,18 @@ Metric: "M=1 FP8-weight GEMV HBM GB/s (% peak); M=256 fused GEMM
 `value` = GB/s of the M=1 decode GEMV on config 2 (K=4096, N=14336, bf16 activations, E4M3FN
 weights ~N(0,0.02) with 0.1% x20 outliers, K-group-128 f32 scales, bf16 out): algorithmic
 bytes (codes + scales + x + y, each crossing HBM once) / average kernel duration, measured with
-HIP events on the stream the kernel runs on. The same line carries the config-3 M=256 MFMA GEMM
-(K=N=8192, fp16 x, per-channel UE8M0, f32 bias) TFLOP/s, the decode sweep M=2/4/8, and the
-reference's CPU forward (dequantize + F.linear in fp32, restated in oracle/cpu_path.py) timed on
-the host cores of the same box.
+HIP events on the stream the kernel runs on. The same line carries every other benchmark
+configuration as its own roofline point (`configs`: C1 M=1, C2 M=2/4/8, C3 M=16/64/256 -- M=256
+also as `gemm_m256` in TFLOP/s and MFMA fraction -- and C4), the C5 tiny-Llama prefill and
+HIP-graph decode (`c5`), FP8Linear.forward's per-call time (`fp8linear_forward_call_us`), the W8A8
+block-32 GEMM, and the reference's CPU forward (dequantize + F.linear in fp32, restated in
+oracle/cpu_path.py) timed on every host CPU available to the process for C1, C2 M=1, C3 M=256
+and C4 (`cpu_baselines`; `cpu_baseline` is the headline's).
 
 Weights rotate over >= 512 MiB of distinct copies so the 256 MB Infinity Cache cannot serve them.
 A step = one kernel launch over one batch (one copy of the layer). Synthetic data, seeded.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|gemm|c5|w8a8]
 """
 import argparse
 import json
@@ -57,12 +60,37 @@ C4_M, C4_N, C4_K = 128, 4096, 11008
 C4_BYTES = C4_N * C4_K + C4_N * (C4_K // 32) + C4_M * C4_K * 2 + C4_M * C4_N * 2   # 50,364,416
 
 
-def cpu_threads():
+def host_cpu_info():
+    """CPU model, logical CPUs, CPUs this process may run on, and the cgroup CPU quota (if any)."""
+    model = "?"
     try:
-        n = len(os.sched_getaffinity(0))
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        affinity = os.cpu_count() or 1
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "affinity": affinity, "cgroup_quota_cpus": quota}
+
+
+def cpu_threads():
+    """Every CPU this process can actually use: its affinity set, bounded by the cgroup quota."""
+    info = host_cpu_info()
+    n = info["affinity"]
+    if info["cgroup_quota_cpus"]:
+        n = min(n, max(1, int(info["cgroup_quota_cpus"])))
+    return max(1, n)
 
 
 class Layer:
@@ -180,9 +208,11 @@ def time_layers(layers, steps, warmup):
     return total / steps
 
 
-def cpu_baseline(q, s, x, bias, G, fmt, nbytes, rounds=5):
-    """The reference CPU forward (oracle/cpu_path.py) on the host cores: one full C2 M=1 layer call
-    per round (weight re-materialised each call, as the reference does)."""
+def cpu_baseline(label, q, s, x, bias, G, fmt, out_dtype, nbytes, flops, rounds=7, warmup=2):
+    """The reference CPU forward (oracle/cpu_path.py: dequantize to fp32, then F.linear, per call,
+    as tfp8/linear.py:179-181 does) on every host CPU this process may use, timed with
+    time.perf_counter: `warmup` untimed calls, then the median of `rounds` (the method of the
+    reference's tests/bench_cpu_transcode.py:145-164)."""
     import torch
 
     from oracle import cpu_path
@@ -192,14 +222,69 @@ def cpu_baseline(q, s, x, bias, G, fmt, nbytes, rounds=5):
     bc = bias.cpu() if bias is not None else None
     table = cpu_path.lut16(fmt)
     ts = []
-    for i in range(2 + rounds):
+    for i in range(warmup + rounds):
         t = time.perf_counter()
-        cpu_path.cpu_forward(xc, qc, sc, G, fmt, bc, x.dtype, table)
+        cpu_path.cpu_forward(xc, qc, sc, G, fmt, bc, out_dtype, table)
         ts.append(time.perf_counter() - t)
-    med = statistics.median(ts[2:])
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": th, "kind": "port",
-            "sample": f"full C2 M=1 layer forward (14336x4096 E4M3FN G128, bf16 x), median of {rounds} "
-                      f"rounds after 2 warm-ups, {med * 1e3:.1f} ms/call"}
+    med = statistics.median(ts[warmup:])
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "tflops": round(flops / med / 1e12, 4),
+            "ms_per_call": round(med * 1e3, 2), "cores": th, "kind": "port",
+            "sample": f"{label}: one full layer forward per round (weight re-dequantized each call, as the "
+                      f"reference does), median of {rounds} rounds after {warmup} warm-ups"}
+
+
+def forward_call_us(layer_data, M, calls=200):
+    """FP8Linear.forward per Python call on this layer (tfp8/linear.py:150-208 is the reference's
+    per-call path; its own figure is ~17 us at M=1, linear.py:173-176): host time per call with the
+    calls enqueued back to back, and the synchronised wall time per call."""
+    import torch
+
+    from tfp8.linear import FP8Linear
+    q, s, x1, bias, G, fmt = layer_data
+    layer = FP8Linear.from_fp8_checkpoint(q, s, bias, fmt=fmt, out_dtype=x1.dtype)
+    x = x1[:1].expand(M, -1).contiguous() if x1.shape[0] < M else x1[:M].contiguous()
+    for _ in range(10):
+        layer(x)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(calls):
+        layer(x)
+    host = time.perf_counter() - t
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t
+    return {"host_us": round(host / calls * 1e6, 2), "wall_us": round(wall / calls * 1e6, 2)}
+
+
+def bench_c5(batches=(1, 8), prompt_len=512, n_decode=128):
+    """the tiny Llama (8 layers, d=2048, 16 heads, FFN 5632, vocab 32000, random N(0,0.02)
+    init), every Linear an E4M3FN per-channel FP8Linear: prefill 512 tokens, then greedy decode of
+    128 tokens at B=1 and B=8, decode replayed from one captured HIP graph per token (the
+    reference times the same loop eagerly, tfp8/examples/demo_llm.py:140-152, 186-200)."""
+    import torch
+
+    from tfp8 import FP8Config, prepare_model
+    from tfp8.examples import demo_llm as D
+    from tfp8.linear import FP8Linear
+    c = D.SIZES["c5"]
+    model = D.build("c5")
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn", weight_group=None, nan_check=True))
+    layers = [m for m in model.modules() if isinstance(m, FP8Linear)]
+    wbytes = sum(m.qweight.numel() + m.weight_scale.numel() * m.weight_scale.element_size() for m in layers)
+    out = {"workload": "C5 tiny Llama, 8 layers d=2048 16 heads FFN 5632 vocab 32000, E4M3FN per-channel "
+                       "FP8Linear, prefill 512 + 128 greedy decode steps, HIP-graph decode",
+           "fp8_linear_layers": len(layers), "fp8_weight_bytes_per_step": wbytes}
+    for B in batches:
+        p, d, pg, dg = D.timings(model, B, prompt_len, n_decode, c["vocab"])
+        out[f"B{B}"] = {"prefill_ms_eager": round(p, 3), "prefill_ms_graph": round(pg, 3),
+                        "decode_ms_per_token_eager": round(d, 4), "decode_ms_per_token_graph": round(dg, 4),
+                        "decode_tokens_per_s": round(B / dg * 1e3, 1),
+                        "prefill_tokens_per_s": round(B * prompt_len / pg * 1e3, 1),
+                        "fp8_weight_gbs": round(wbytes / (dg * 1e-3) / 1e9, 1),
+                        "frac_of_hbm_roofline": round(wbytes / (dg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"[bench] C5 B={B}: {out[f'B{B}']}")
+    del model
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_w8a8(dev, steps, M=8192, N=8192, K=8192):
@@ -256,14 +341,27 @@ def read_traffic():
     return None
 
 
+def _point(layers, nbytes, flops, steps, warmup, runs=1):
+    """Average launch duration (median of `runs` timed runs) and its roofline figures."""
+    ts = sorted(time_layers(layers, steps, warmup) for _ in range(runs))
+    t = ts[len(ts) // 2]
+    gbs, tf = nbytes / t / 1e9, flops / t / 1e12
+    bound = "mfma" if flops / nbytes > PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9) else "hbm"
+    frac = tf / PEAK_F16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+    return {"us": round(t * 1e6, 3), "gbs": round(gbs, 1), "tflops": round(tf, 2), "bound": bound,
+            "frac": round(frac, 4), "algorithmic_bytes": nbytes, "flops": int(flops),
+            **({"runs_us": [round(r * 1e6, 2) for r in ts]} if runs > 1 else {})}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "w8a8"], default=None)
-    ap.add_argument("--sweep", action="store_true", help="also time the C2 decode sweep M=2,4,8 and C3 M=16,64")
+    ap.add_argument("--no-calls", action="store_true", help="skip the FP8Linear.forward per-call timing (its "
+                    "kernels reread one weight copy, so they would mix into a kernel trace of the timed launches)")
+    ap.add_argument("--only", choices=["gemv", "gemm", "w8a8", "c5"], default=None)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run torch copies of a 256 MiB buffer (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -279,7 +377,6 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    out = {}
     if a.calibrate_copy:
         src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -289,113 +386,126 @@ def main():
         log("[bench] calibration: 5 copies of 268435456 bytes (read + write each)")
         return
 
-    # ---------------------------------------------------------------- C2 M=1 GEMV (headline)
+    pts, cpu, calls, out = {}, {}, {}, {}
+    gemm_steps = max(20, a.steps // 2)
+    # ---------------------------------------------------------------- decode GEMVs: C2 M=1 (headline), C1, C2 sweep
     if a.only in (None, "gemv"):
         log("[bench] C2 M=1 GEMV: building rotating weights")
-        layers, (q, s, x, bias, G, fmt), meta = make_layers("c2", 1, dev)
-        mean = time_layers(layers, a.steps, a.warmup)
-        nb = c2_bytes(1)
-        gbs = nb / mean / 1e9
-        log(f"[bench] C2 M=1: {mean * 1e6:.2f} us/launch -> {gbs:.1f} GB/s")
-        out["gemv"] = dict(mean=mean, bytes=nb, gbs=gbs, meta=meta)
-        l1, _, _ = make_layers("c1", 1, dev)
-        m1 = time_layers(l1, a.steps, a.warmup)
-        out["c1"] = dict(us=m1 * 1e6, gbs=c1_bytes(1) / m1 / 1e9)
-        log(f"[bench] C1 M=1: {m1 * 1e6:.2f} us/launch -> {out['c1']['gbs']:.1f} GB/s")
-        del l1
-        if a.sweep:
-            sweep = {}
-            for M in (2, 4, 8):
-                lm, _, _ = make_layers("c2", M, dev)
-                mm = time_layers(lm, a.steps, a.warmup)
-                sweep[f"M{M}"] = round(c2_bytes(M) / mm / 1e9, 1)
-                log(f"[bench] C2 M={M}: {mm * 1e6:.2f} us -> {sweep[f'M{M}']} GB/s")
-                del lm
-            out["sweep"] = sweep
+        layers, c2data, meta = make_layers("c2", 1, dev)
+        pts["c2_m1"] = _point(layers, c2_bytes(1), 2.0 * 14336 * 4096, a.steps, a.warmup)
+        log(f"[bench] C2 M=1: {pts['c2_m1']}")
+        out["gemv_meta"] = meta
+        if not a.no_calls:
+            calls["c2_m1"] = forward_call_us(c2data, 1)
         if not a.no_cpu:
-            log("[bench] CPU baseline (reference CPU forward)")
-            out["cpu"] = cpu_baseline(q, s, x, bias, G, fmt, nb)
-            log(f"[bench] CPU: {out['cpu']}")
+            q, s_, x, bias, G, fmt = c2data
+            cpu["c2_m1"] = cpu_baseline("C2 M=1 (14336x4096 E4M3FN G128, bf16 x)", q, s_, x, bias, G, fmt,
+                                        torch.bfloat16, c2_bytes(1), 2.0 * 14336 * 4096)
+            log(f"[bench] CPU C2 M=1: {cpu['c2_m1']}")
         del layers
+        for M in (2, 4, 8):
+            lm, _, _ = make_layers("c2", M, dev)
+            pts[f"c2_m{M}"] = _point(lm, c2_bytes(M), 2.0 * M * 14336 * 4096, a.steps, a.warmup)
+            log(f"[bench] C2 M={M}: {pts[f'c2_m{M}']}")
+            del lm
+        l1, c1data, _ = make_layers("c1", 1, dev)
+        pts["c1_m1"] = _point(l1, c1_bytes(1), 2.0 * 4096 * 4096, a.steps, a.warmup)
+        log(f"[bench] C1 M=1: {pts['c1_m1']}")
+        if not a.no_calls:
+            calls["c1_m1"] = forward_call_us(c1data, 1)
+        if not a.no_cpu:
+            q, s_, x, bias, G, fmt = c1data
+            cpu["c1_m1"] = cpu_baseline("C1 M=1 (4096x4096 E4M3FN per-channel, fp16 x)", q, s_, x, bias, G, fmt,
+                                        torch.float16, c1_bytes(1), 2.0 * 4096 * 4096)
+            log(f"[bench] CPU C1: {cpu['c1_m1']}")
+        del l1
         torch.cuda.empty_cache()
 
-    # ---------------------------------------------------------------- C3 M=256 GEMM
+    # ---------------------------------------------------------------- GEMMs: C3 M=16/64/256, C4
     if a.only in (None, "gemm"):
-        log("[bench] C3 M=256 GEMM: building rotating weights")
-        layers, _, meta3 = make_layers("c3", 256, dev)
-        steps = max(20, a.steps // 2)
-        # median of three timed runs: single runs of this ~50 us launch vary by several percent
-        runs3 = sorted(time_layers(layers, steps, max(5, a.warmup // 2)) for _ in range(3))
-        mean3 = runs3[1]
-        fl = 2.0 * 256 * 8192 * 8192
-        tf = fl / mean3 / 1e12
-        log(f"[bench] C3 M=256: kernel {mean3 * 1e6:.2f} us -> {tf:.1f} TFLOP/s ({c3_bytes(256) / mean3 / 1e9:.0f} GB/s)")
-        out["gemm"] = dict(mean=mean3, tflops=tf, meta=meta3, runs_us=[round(r * 1e6, 2) for r in runs3])
-        gsweep = {}
-        for M in ((16, 64) if a.sweep else ()):
-            lm, _, _ = make_layers("c3", M, dev)
-            mm = time_layers(lm, steps, 5)
-            gsweep[f"M{M}"] = {"us": round(mm * 1e6, 2), "gbs": round(c3_bytes(M) / mm / 1e9, 1),
-                               "tflops": round(2.0 * M * 8192 * 8192 / mm / 1e12, 1)}
-            log(f"[bench] C3 M={M}: {gsweep[f'M{M}']}")
+        for M in (16, 64, 256):
+            log(f"[bench] C3 M={M} GEMM: building rotating weights")
+            lm, c3data, meta3 = make_layers("c3", M, dev)
+            # median of three timed runs: single runs of the ~50 us launches vary by several percent
+            pts[f"c3_m{M}"] = _point(lm, c3_bytes(M), 2.0 * M * 8192 * 8192, gemm_steps, max(5, a.warmup // 2),
+                                     runs=3)
+            log(f"[bench] C3 M={M}: {pts[f'c3_m{M}']}")
+            if M == 16 and not a.no_calls:
+                calls["c3_m16"] = forward_call_us(c3data, 16)
+            if M == 256:
+                out["gemm_meta"] = meta3
+                if not a.no_cpu:
+                    q, s_, x, bias, G, fmt = c3data
+                    cpu["c3_m256"] = cpu_baseline("C3 M=256 (8192x8192 E4M3FN per-channel UE8M0, fp16 x)", q, s_, x,
+                                                  bias, G, fmt, torch.float16, c3_bytes(256),
+                                                  2.0 * 256 * 8192 * 8192)
+                    log(f"[bench] CPU C3 M=256: {cpu['c3_m256']}")
             del lm
-        out["gemm_sweep"] = gsweep
-        del layers
+            torch.cuda.empty_cache()
         log("[bench] C4 M=128 GEMM (E5M2, UE8M0 32-groups): building rotating weights")
-        l4, _, meta4 = make_layers("c4", C4_M, dev)
-        m4 = sorted(time_layers(l4, steps, 5) for _ in range(3))[1]
-        out["c4"] = {"us": round(m4 * 1e6, 2), "gbs": round(C4_BYTES / m4 / 1e9, 1),
-                     "tflops": round(2.0 * C4_M * C4_N * C4_K / m4 / 1e12, 1), "timing": "median of 3 runs"}
-        log(f"[bench] C4 M=128: {out['c4']}")
+        l4, c4data, _ = make_layers("c4", C4_M, dev)
+        pts["c4_m128"] = _point(l4, C4_BYTES, 2.0 * C4_M * C4_N * C4_K, gemm_steps, 5, runs=3)
+        log(f"[bench] C4 M=128: {pts['c4_m128']}")
+        if not a.no_cpu:
+            q, s_, x, bias, G, fmt = c4data
+            cpu["c4_m128"] = cpu_baseline("C4 M=128 (4096x11008 E5M2 G32 UE8M0, bf16 x)", q, s_, x, bias, G, fmt,
+                                          torch.bfloat16, C4_BYTES, 2.0 * C4_M * C4_N * C4_K)
+            log(f"[bench] CPU C4: {cpu['c4_m128']}")
         del l4
+        torch.cuda.empty_cache()
 
-    # ---------------------------------------------------------------- W8A8 block-32 GEMM
+    # ---------------------------------------------------------------- C5 tiny Llama, W8A8
+    if a.only in (None, "c5"):
+        out["c5"] = bench_c5()
     if a.only in (None, "w8a8"):
         out["w8a8"] = bench_w8a8(dev, max(10, a.steps // 10))
 
-    g = out.get("gemv")
+    g = pts.get("c2_m1")
     line = {
         "metric": "M=1 FP8-weight GEMV HBM GB/s (% peak); M=256 fused GEMM TFLOP/s",
-        "value": round(g["gbs"], 1) if g else None,
+        "value": g["gbs"] if g else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(g["mean"] * 1e3, 5) if g else None,
+        "ms_per_step": round(g["us"] * 1e-3, 5) if g else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "C2 decode GEMV M=1: K=4096 N=14336, bf16 x, E4M3FN weights (0.1% x20 outliers), "
-                               "K-group-128 f32 scales, bf16 out",
-                   **({k: v for k, v in g["meta"].items()} if g else {})},
+                               "K-group-128 f32 scales, bf16 out", **out.get("gemv_meta", {})},
     }
     if g:
         line["pct_peak_hbm"] = round(100 * g["gbs"] / PEAK_HBM_GBS, 1)
-        line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                            "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
-                            "kernel_us": round(g["mean"] * 1e6, 3), "algorithmic_bytes": g["bytes"]}
-        line["config1_m1"] = {"us": round(out["c1"]["us"], 2), "gbs": round(out["c1"]["gbs"], 1),
-                              "frac": round(out["c1"]["gbs"] / PEAK_HBM_GBS, 4)}
-        if "sweep" in out:
-            line["decode_sweep_gbs"] = out["sweep"]
-    if "gemm" in out:
-        gm = out["gemm"]
-        line["gemm_m256"] = {"tflops": round(gm["tflops"], 1), "kernel_us": round(gm["mean"] * 1e6, 2),
-                             "runs_us": gm["runs_us"], "timing": "median of 3 runs, GEMM + split-K reduce",
-                             "roofline": {"bound": "mfma", "achieved": round(gm["tflops"], 1),
-                                          "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                                          "frac": round(gm["tflops"] / PEAK_F16_TFLOPS, 4)},
+        line["roofline"] = {"bound": "hbm", "achieved": g["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": g["frac"], "traffic": read_traffic(),
+                            "traffic_source": "profiles/traffic_gemv_c2_m1.txt: rocprofv3 --pmc FETCH_SIZE and "
+                                              "WRITE_SIZE of this kernel on an earlier run (not measured in this run)",
+                            "kernel_us": g["us"], "algorithmic_bytes": g["algorithmic_bytes"]}
+    if "c3_m256" in pts:
+        gm = pts["c3_m256"]
+        line["gemm_m256"] = {"tflops": gm["tflops"], "kernel_us": gm["us"], "runs_us": gm["runs_us"],
+                             "timing": "median of 3 runs, every kernel of the call (GEMM and split-K reduce)",
+                             "roofline": {"bound": "mfma", "achieved": gm["tflops"], "peak": PEAK_F16_TFLOPS,
+                                          "unit": "TFLOP/s", "frac": gm["frac"]},
                              "config": {"workload": "C3 fused GEMM M=256: K=N=8192, fp16 x, E4M3FN, per-channel "
-                                                    "UE8M0, f32 bias, fp16 out", **gm["meta"]}}
-        if out.get("gemm_sweep"):
-            line["gemm_sweep"] = out["gemm_sweep"]
-        if out.get("c4"):
-            line["c4_gemm"] = out["c4"]
+                                                    "UE8M0, f32 bias, fp16 out", **out.get("gemm_meta", {})}}
+    line["configs"] = pts
+    if calls:
+        line["fp8linear_forward_call_us"] = calls
+    if "c5" in out:
+        line["c5"] = out["c5"]
     if "w8a8" in out:
         line["w8a8"] = out["w8a8"]
-    line["cpu_baseline"] = out.get("cpu")
+    if cpu:
+        host = host_cpu_info()
+        for v in cpu.values():
+            v["cpu_model"] = host["model"]
+        line["cpu_host"] = host
+        line["cpu_baselines"] = cpu
+    line["cpu_baseline"] = cpu.get("c2_m1")
     print(json.dumps(line), flush=True)
 
 
