@@ -11,6 +11,8 @@ void run_gemv_bf16(const void*, int, int, const uint8_t*, int, const void*, int,
 void run_gemv_f32(const void*, int, int, const uint8_t*, int, const void*, int, int, int, const float*, void*, int, int,
                   int, hipStream_t);
 
+int run_gemv_pair(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
+                  int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
 int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, const uint8_t* w, int N, const void* ws,
                   int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
 
@@ -21,6 +23,10 @@ int gemv_mfma_min_m() { return tune(TUNE_GEMV_MFMA_MIN); }
 
 int run_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind, int G,
              int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
+    if (M == 1) {
+        const int rc = run_gemv_pair(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
+        if (rc != NOT_TAKEN) return rc;
+    }
     if (M >= gemv_mfma_min_m()) {
         const int rc = run_gemv_mfma(x, x_dtype, nullptr, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rc != NOT_TAKEN) return rc;

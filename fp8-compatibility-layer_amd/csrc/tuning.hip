@@ -41,6 +41,7 @@ constexpr KnobDef KNOBS[TUNE_COUNT] = {
     {"TFP8_GS_SPLITK", 0},           // weight-streaming GEMM split-K (0: by shape)
     {"TFP8_GS_TL", 1},               // weight-streaming GEMM: transposed weight loads
     {"TFP8_GEMM_V1", 0},             // skip the weight-streaming GEMM (LDS-tiled kernel instead)
+    {"TFP8_GEMV_PAIR", 1},           // M = 1: row-pair GEMV where it applies (0 off, 1 auto, 4/8 waves per block)
 };
 
 std::atomic<int> g_knob[TUNE_COUNT];

@@ -158,7 +158,7 @@ int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, i
  * Kernel-selection overrides for sweeps and for tests that force every compiled configuration:
  * TFP8_GEMV_CFG, TFP8_GEMV_WPC, TFP8_GEMV_MFMA_MIN, TFP8_GEMV_MFMA_MAX_M, TFP8_GM_NT, TFP8_GM_W,
  * TFP8_GM_D, TFP8_GM_TL, TFP8_GEMM_TILE, TFP8_GEMM_SPLITK, TFP8_GEMM_DIRECT, TFP8_GEMM_DIRECT_MIN_M,
- * TFP8_GEMM_DCFG, TFP8_GS_NW, TFP8_GS_KCS, TFP8_GS_SPLITK, TFP8_GS_TL, TFP8_GEMM_V1.  Each starts at
+ * TFP8_GEMM_DCFG, TFP8_GS_NW, TFP8_GS_KCS, TFP8_GS_SPLITK, TFP8_GS_TL, TFP8_GEMM_V1, TFP8_GEMV_PAIR.  Each starts at
  * the value of the environment variable of that name when the library is loaded (or its default),
  * and changes only through tfp8_tuning_set; the launch path never reads the environment.  A knob
  * changes routing and workspace sizes for every later call in the process: size workspaces after

@@ -68,6 +68,13 @@ def test_kernel_switch_points_and_tails():
         _run(M, 200, 512, None, torch.float16)
 
 
+def test_streaming_gemv_m1_where_pair_applies(tune):
+    """M = 1 shapes the row-pair GEMV would take, forced through the streaming GEMV instead."""
+    tune(TFP8_GEMV_PAIR=0)
+    for N, K, G in ((14336, 4096, 128), (4096, 4096, None), (999, 2048, 64)):
+        _run(1, N, K, G, torch.bfloat16, seed=N + K)
+
+
 def test_kernel_ragged_k_tail():
     for K in (528, 1040, 1152, 1168, 1184):
         for M in (1, 8, 16, 64):
@@ -427,6 +434,49 @@ def test_decode_mfma_every_config(nt, w, d, tune):
     # 9..16 rows (the GEMM entry): bf16 activations, and fp32 ones prepared to f16 with row scales
     _run(16, 136, 256 * w * 2, 64, torch.bfloat16, xdt=torch.bfloat16, seed=nt + 16)
     _run(11, 200, 1152, None, torch.float32, xdt=torch.float32, seed=d + 11)
+
+
+@pytest.mark.parametrize("wpb", [1, 4, 8])
+def test_row_pair_gemv_shapes(wpb, tune):
+    """The row-pair GEMV (M = 1, K = 2048/4096/8192) with 4 or 8 waves per block and the automatic
+    choice: per-channel and K-group (64/128/256, where a lane group reduces before its scale)
+    scales in f32 and UE8M0, both formats, f16/bf16 activations, every output dtype, with and
+    without bias, N odd (a half pair at the end) and below one block."""
+    tune(TFP8_GEMV_PAIR=wpb)
+    cases = [(14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
+             (4096, 4096, None, "e4m3fn", "f32", torch.float16, torch.float16, False),
+             (1001, 2048, 64, "e5m2", "ue8m0", torch.bfloat16, torch.float32, True),
+             (999, 8192, 256, "e4m3fn", "f32", torch.float16, torch.float32, True),
+             (37, 8192, None, "e5m2", "ue8m0", torch.bfloat16, torch.bfloat16, True),
+             (514, 2048, 128, "e4m3fn", "ue8m0", torch.float16, torch.float16, True),
+             (3, 4096, 128, "e5m2", "f32", torch.bfloat16, torch.float32, True)]
+    for i, (N, K, G, fmt, sf, xdt, out, bias) in enumerate(cases):
+        _run(1, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=wpb * 100 + i)
+
+
+def test_row_pair_gemv_matches_streaming_gemv(tune):
+    """The same M = 1 products through the row-pair GEMV and the streaming GEMV (which the pair
+    kernel replaced for these shapes): both within the oracle tolerance and within a few f32
+    ulps of each other (only the summation order differs); a 2-byte-offset output, which the
+    pair store cannot take, falls back to the streaming kernel."""
+    q, s, G, b = _layer(4104, 4096, 128, "e4m3fn", "f32", False, seed=5)
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(6)).bfloat16().cuda()
+    outs = []
+    for pair in (0, 1):
+        tune(TFP8_GEMV_PAIR=pair)
+        outs.append(_ext.w8a16(x, q, None, s, b, torch.float32, G, "e4m3fn"))
+    torch.cuda.synchronize()
+    for y in outs:
+        _check(y, x, q, s, G, "e4m3fn", b, torch.float32, "gemv", "pair vs streaming")
+    assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-5)
+    lib = _ext.require()
+    ybuf = torch.zeros(4104 + 1, dtype=torch.bfloat16, device="cuda")
+    y = ybuf[1:]
+    assert y.data_ptr() % 4 == 2
+    rc = lib.tfp8_gemv(x.data_ptr(), _ext.DTYPE_ID[x.dtype], 1, 4096, q.data_ptr(), 4104, s.data_ptr(), 0, G, 0,
+                       b.data_ptr(), y.data_ptr(), _ext.DTYPE_ID[torch.bfloat16], torch._C._cuda_getCurrentRawStream(0))
+    assert rc == 0
+    _check(y.view(1, -1), x, q, s, G, "e4m3fn", b, torch.bfloat16, "gemv", "misaligned y")
 
 
 @pytest.mark.parametrize("M,N,K,G,sf", [(16, 8192, 8192, None, "ue8m0"), (24, 1000, 2048, 128, "f32"),
