@@ -1,11 +1,13 @@
-"""Symmetric FP8 weight quantization and the activation row scale (API of tfp8/quantize.py:1-62).
+"""Weight quantization to FP8 codes with per-row / per-K-group scales, its inverse, and the
+power-of-two row rescale of activations (functions of the reference's tfp8/quantize.py:1-62).
 
-    scale = max|w| / FP8_MAX   (rounded up to a power of two by default)
-    q     = RNE(clamp(w / scale, -FP8_MAX, FP8_MAX))
-
-Scales are float32, or UE8M0 bytes (scale = 2^(byte-127), always a power of two) when
-`scale_format="ue8m0"`.  CUDA tensors run the gfx950 quantize / dequant / prep kernels; CPU
-tensors run the torch code here, which computes the same numbers.
+For every weight row n and group g of G consecutive inputs the scale is the group's largest
+magnitude divided by the format's largest finite value (raised to a power of two unless
+pow2_scale=False; 1 for an all-zero group), and each code is the round-to-nearest-even FP8 value
+of w / scale, saturated at the largest finite code.  Scales are stored as float32, or with
+scale_format="ue8m0" as one byte e per scale meaning 2^(e-127).  On a CUDA tensor the gfx950
+kernels (quantize, dequant, prep) do the work; on a CPU tensor the torch code below does, with
+identical results.
 """
 import torch
 
@@ -44,12 +46,12 @@ def scale_values(s: torch.Tensor) -> torch.Tensor:
 
 
 def quantize_weight(w: torch.Tensor, fmt="e4m3fn", group_size=None, pow2_scale=True, scale_format="f32"):
-    """w [N,K] -> (qweight uint8 [N,K], scale [N, K/G], G).
+    """Quantize a [N, K] weight: returns (codes uint8 [N, K], scales [N, K // G], G).
 
-    group_size None -> one scale per output channel (G = K). scale is float32, or uint8 UE8M0
-    bytes for scale_format="ue8m0" (which implies power-of-two scales).
-    Runs on whatever device w lives on; call it layer by layer so the full-precision model
-    never has to sit in VRAM next to the quantized one.
+    G = K (one scale per output row) when group_size is None.  Scales come back as float32, or as
+    UE8M0 bytes for scale_format="ue8m0", which always uses power-of-two scales.  The work happens
+    on w's device, so a model can be converted one layer at a time without holding a second
+    full-precision copy.
     """
     f = get_format(fmt)
     if scale_format not in SCALE_FORMATS:
@@ -84,14 +86,15 @@ def dequantize_weight(q: torch.Tensor, s: torch.Tensor, fmt, group_size) -> torc
     return (v * scale_values(s)[..., None]).reshape(N, K)
 
 
-ACT_TARGET_EXP = 8  # row amax is mapped into [2^7, 2^8): far from fp16 overflow, ~30 binades of headroom
+ACT_TARGET_EXP = 8  # a row's largest magnitude lands in (2^7, 2^8]: fp16 keeps ~7 binades above it, ~30 below
 
 
 def activation_to_fp16(x: torch.Tensor):
-    """BF16/FP32 activation rows -> (fp16 [M,K], power-of-two row scale f32 [M]).
+    """Rescale each activation row by a power of two so it fits fp16: returns (x16 fp16 [M, K],
+    xs f32 [M]) with x = x16 * xs.
 
-    Dividing by an exact power of two is lossless, so BF16 -> FP16 only loses values that
-    would land in fp16's subnormal range. FP16 input passes through.
+    The division by 2^e is exact, so only entries far below the row maximum (in fp16's subnormal
+    range after the shift) lose bits.  fp16 rows are returned unchanged with xs = 1.
     """
     if x.dtype == torch.float16:
         return x.contiguous(), torch.ones(x.shape[0], dtype=torch.float32, device=x.device)
