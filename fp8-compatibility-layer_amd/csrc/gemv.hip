@@ -23,7 +23,7 @@ int gemv_mfma_min_m() { return tune(TUNE_GEMV_MFMA_MIN); }
 
 int run_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind, int G,
              int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
-    if (M == 1) {
+    {
         const int rc = run_gemv_pair(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rc != NOT_TAKEN) return rc;
     }

@@ -41,7 +41,8 @@ constexpr KnobDef KNOBS[TUNE_COUNT] = {
     {"TFP8_GS_SPLITK", 0},           // weight-streaming GEMM split-K (0: by shape)
     {"TFP8_GS_TL", 1},               // weight-streaming GEMM: transposed weight loads
     {"TFP8_GEMM_V1", 0},             // skip the weight-streaming GEMM (LDS-tiled kernel instead)
-    {"TFP8_GEMV_PAIR", 1},           // M = 1: row-pair GEMV where it applies (0 off, 1 auto, 4/8 waves per block)
+    {"TFP8_GEMV_PAIR", 1},           // row-pair GEMV where it applies (0 off, 1 auto, 4/8 waves per block at M = 1)
+    {"TFP8_GEMV_PAIR_MAX_M", 4},     // largest M (1..4) for the row-pair GEMV
 };
 
 std::atomic<int> g_knob[TUNE_COUNT];

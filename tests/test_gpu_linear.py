@@ -69,10 +69,12 @@ def test_kernel_switch_points_and_tails():
 
 
 def test_streaming_gemv_m1_where_pair_applies(tune):
-    """M = 1 shapes the row-pair GEMV would take, forced through the streaming GEMV instead."""
+    """M <= 3 shapes the row-pair GEMV would take, forced through the streaming GEMV instead (and
+    M = 4 through the matrix-core decode kernel)."""
     tune(TFP8_GEMV_PAIR=0)
-    for N, K, G in ((14336, 4096, 128), (4096, 4096, None), (999, 2048, 64)):
-        _run(1, N, K, G, torch.bfloat16, seed=N + K)
+    for M in (1, 2, 3, 4):
+        for N, K, G in ((14336, 4096, 128), (4096, 4096, None), (998, 2048, 64)):
+            _run(M, N, K, G, torch.bfloat16, seed=N + K + M)
 
 
 def test_kernel_ragged_k_tail():
@@ -420,7 +422,7 @@ def test_decode_mfma_every_config(nt, w, d, tune):
     M = 1: rows past N in the last block, a K tail that is not a whole 64-byte chunk, K ranges that
     leave some waves without work, per-channel / f32 K-group (G=64) / UE8M0 K-group (G=32) scales,
     both formats, f16 and bf16 activations, with and without bias."""
-    tune(TFP8_GEMV_MFMA_MIN=1)
+    tune(TFP8_GEMV_MFMA_MIN=1, TFP8_GEMV_PAIR=0)
     tune(TFP8_GM_NT=nt)
     tune(TFP8_GM_W=w)
     tune(TFP8_GM_D=d)
@@ -438,11 +440,20 @@ def test_decode_mfma_every_config(nt, w, d, tune):
 
 @pytest.mark.parametrize("wpb", [1, 4, 8])
 def test_row_pair_gemv_shapes(wpb, tune):
-    """The row-pair GEMV (M = 1, K = 2048/4096/8192) with 4 or 8 waves per block and the automatic
-    choice: per-channel and K-group (64/128/256, where a lane group reduces before its scale)
-    scales in f32 and UE8M0, both formats, f16/bf16 activations, every output dtype, with and
-    without bias, N odd (a half pair at the end) and below one block."""
+    """The row-pair GEMV (M = 1..4, K = 2048/4096/8192; at M = 1 with 4 or 8 waves per block and the
+    automatic choice): per-channel and K-group (64/128/256, each lane's group scale broadcast
+    inside its lane segment) scales in f32 and UE8M0, both formats, f16/bf16 activations, every
+    output dtype, with and without bias, M = 3 on the 4-row kernel, N odd (a half pair at the end
+    at M = 1; not taken at M > 1) and below one block."""
     tune(TFP8_GEMV_PAIR=wpb)
+    for i, (M, N, K, G, fmt, sf, xdt, out, bias) in enumerate([
+            (2, 14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
+            (3, 1000, 2048, 64, "e5m2", "ue8m0", torch.float16, torch.float32, True),
+            (4, 4096, 4096, None, "e4m3fn", "f32", torch.float16, torch.float16, True),
+            (4, 998, 8192, 256, "e5m2", "f32", torch.bfloat16, torch.float32, True),
+            (2, 514, 2048, 128, "e4m3fn", "ue8m0", torch.float16, torch.float16, True),
+            (2, 37, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, True)]):   # N odd, M > 1: not taken
+        _run(M, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=wpb * 1000 + i)
     cases = [(14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
              (4096, 4096, None, "e4m3fn", "f32", torch.float16, torch.float16, False),
              (1001, 2048, 64, "e5m2", "ue8m0", torch.bfloat16, torch.float32, True),
@@ -506,6 +517,7 @@ def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, tune):
     LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
     64 bytes per load): the outputs must be bit-identical."""
     print(f"[linear] decode transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
+    tune(TFP8_GEMV_PAIR=0)
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).bfloat16().cuda()
     outs = []
