@@ -213,23 +213,52 @@ __device__ __forceinline__ void w8_store(f32x4 (&acc)[TI][TJ], const void* sa, c
     }
 }
 
-// ---- exact kernel for FP32 block scales: f16 tiles in LDS.  128 x 128 tile, 8 waves of 64 x 32
-// (two per SIMD, so one wave's fp32 scale arithmetic overlaps another's MFMAs), K steps of 64: the
-// codes are decoded to f16 once per block on their way into a double-buffered LDS pair
-// (2 x 2 x 16 KB).  A row of a tile is 64 halves = 8 chunks of 8; chunk u of row r sits at
-// u ^ ((r >> 1) & 7), so the 16 rows one fragment read touches land on distinct bank groups.  Lane
-// l of an MFMA for scale block q reads row l & 15, chunk 4q + (l >> 4): k = 32q + 8 (l >> 4) + 0..7,
-// the instruction's own k order.  Each MFMA result (one 32-block of a 16 x 16 tile) is multiplied
-// by sa * sb and added to the fp32 accumulator (fp8_gemm_kernel.cu:74-93).  The first version (4
-// waves of 64 x 64, 128-wide K steps, 128 KB of LDS: one wave per SIMD) computed the same sums
-// in 3061.5 us against 2717.4 us at 8192^3 (same box).
+// ---- exact kernel for FP32 block scales: f16 tiles in LDS.  128 x 128 tile, 8 waves of 64 x 32,
+// K steps of 64.  The codes are decoded to f16 once per block on their way into a double-buffered
+// LDS pair (2 x 2 x 16 KB); a row of a tile is 64 halves = 8 chunks of 8, chunk u of row r at
+// u ^ ((r >> 1) & 7), so the 16 rows one fragment read touches land on distinct bank groups.
+// Lane l of an MFMA for scale block q reads row l & 15, chunk 4q + (l >> 4): k = 32q + 8 (l >> 4)
+// + 0..7, the instruction's own k order.  Each MFMA result (one 32-block of a 16 x 16 tile) is
+// multiplied by sa * sb and added to the fp32 accumulator (fp8_gemm_kernel.cu:74-93: the product
+// sa * sb rounded to fp32, then one fused multiply-add, as racc += partial * s).
+//
+// The scale arithmetic (two VALU ops per output element and 32-block) is what bounds this kernel,
+// so the step is built to keep the VALU fed and the register count at 124 (two blocks per CU, four
+// waves per SIMD):
+//   * the A scales of a step take one 8-byte LDS read per lane: lane (g, k) (g = lane >> 4,
+//     k = lane & 15) holds the (q = 0, 1) pair of row 16 (k >> 2) + 4 g + (k & 3) of the wave tile,
+//     and the multiply for row tile i, value r of any lane in lane row g takes it from lane
+//     k = 4 i + r of its row of 16 with DPP row_newbcast inside the v_mul_f32 itself;
+//   * the MFMAs of row tile i + 1 are issued between the multiply-adds of row tile i (pinned with
+//     scheduling barriers), and row tile i + 2's fragments are read from LDS during row tile i;
+//   * the K loop is unrolled by two, so each step's LDS buffer is a constant and every LDS address
+//     a loop-invariant register plus an immediate; global loads take loop-invariant lane offsets
+//     with the K position in soffset, bounds-checked only for a partial last tile.
+// 8192^3 on one box: 2650 us for the previous form of this kernel (four A-scale LDS reads per
+// row tile, MFMA results consumed right after each MFMA, 154 VGPRs: one block per CU) against
+// 1915-1945 us, bit-identical outputs over the parity shapes.
+
+// sa(lane n of this lane's row of 16) * sb as one v_mul_f32_dpp with row_newbcast:n; n is a
+// constant after unrolling.  sa comes straight from an LDS read (no VALU write feeds the DPP read).
+__device__ __forceinline__ float w8_mul_bcast(float sa, float sb, int n) {
+    float r;
+    switch (n) {
+#define W8_RB(k) case k: asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:" #k " row_mask:0xf bank_mask:0xf bound_ctrl:1" \
+                             : "=v"(r) : "v"(sa), "v"(sb)); break;
+        W8_RB(0) W8_RB(1) W8_RB(2) W8_RB(3) W8_RB(4) W8_RB(5) W8_RB(6) W8_RB(7)
+        W8_RB(8) W8_RB(9) W8_RB(10) W8_RB(11) W8_RB(12) W8_RB(13) W8_RB(14) default: W8_RB(15)
+#undef W8_RB
+    }
+    return r;
+}
+
 template <int FA, int FB>
 __global__ __launch_bounds__(512) void w8_f16_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ sa, const uint8_t* __restrict__ bt,
     const float* __restrict__ sb, const float* __restrict__ bias, float* __restrict__ c, int M, int N, int K) {
     constexpr int BT = 128, WM = 2, WN = 4, WTM = BT / WM, WTN = BT / WN, TI = WTM / 16, TJ = WTN / 16;
     constexpr int NT = 64 * WM * WN, KS = 64, CH = BT * (KS / 16) / NT;
-    static_assert(CH >= 1 && 2 * BT * 2 == NT, "one chunk sweep per operand, one scale word per thread");
+    static_assert(CH == 1 && 2 * BT * 2 == NT && TI == 4, "one chunk per thread and operand, one scale word per thread");
     __shared__ __attribute__((aligned(16))) uint8_t sT[2][2][BT * 128];   // [buffer][A, Bt][row * 128 B]
     __shared__ __attribute__((aligned(16))) float sS[2][2][BT * 2];       // [buffer][A, Bt][row * 2 + q]
 
@@ -250,45 +279,45 @@ __global__ __launch_bounds__(512) void w8_f16_kernel(
     rss[1] = __builtin_amdgcn_make_buffer_rsrc((void*)(sb + (size_t)n0 * nkb), (short)0,
                                                (int)(rows[1] * (uint32_t)nkb * 4u), (int)W8_FLAGS);
 
-    // Chunk ch = tid + i * NT of an operand: row ch >> 2, codes k = kt + 16 (ch & 3) .. +15.  Scale
-    // word: threads 0..255 take A's, 256..511 Bt's (the operand is wave-uniform); word w = tid & 255
-    // is row w >> 1, block kt / 32 + (w & 1).  Past K and past the block's rows the loads read zeros
-    // (zero codes, zero scales).
+    // Thread tid loads codes k = kt + 16 (tid & 3) .. +15 of row tid >> 2 of both operands, and one
+    // scale word: threads 0..255 A's, 256..511 Bt's (the operand is wave-uniform), word w = tid & 255
+    // = row w >> 1, block kt / 32 + (w & 1).  Past K and past the block's rows the loads read zeros.
     const int s_op = wave >> 2, s_w = tid & 255;
-    uint4 rt[2][CH];
+    const int ld_row = tid >> 2, ld_k = 16 * (tid & 3);
+    const uint32_t ld_off = (uint32_t)ld_row * (uint32_t)K + (uint32_t)ld_k;
+    const uint32_t sc_off = (uint32_t)(((s_w >> 1) * nkb + (s_w & 1)) * 4);
+    uint4 rt[2];
     float rsc;
     auto load = [&](int kt) {
+        if (kt + KS <= K) {   // a whole tile: no per-lane bounds
 #pragma unroll
-        for (int op = 0; op < 2; ++op) {
+            for (int op = 0; op < 2; ++op)
+                rt[op] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)ld_off, kt, 0));
+            rsc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rss[s_op], (int)sc_off, (kt / 32) * 4, 0));
+        } else {
+            const uint32_t off = kt + ld_k < K ? ld_off + (uint32_t)kt : W8_OOB;
 #pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                const int ch = tid + i * NT, row = ch >> 2, k = kt + 16 * (ch & 3);
-                const uint32_t off = k < K ? (uint32_t)row * (uint32_t)K + (uint32_t)k : W8_OOB;
-                rt[op][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)off, 0, 0));
-            }
+            for (int op = 0; op < 2; ++op)
+                rt[op] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[op], (int)off, 0, 0));
+            const uint32_t o = kt / 32 + (s_w & 1) < nkb ? sc_off + (uint32_t)((kt / 32) * 4) : W8_OOB;
+            rsc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rss[s_op], (int)o, 0, 0));
         }
-        const int row = s_w >> 1, kb = kt / 32 + (s_w & 1);
-        const uint32_t o = kb < nkb ? (uint32_t)((row * nkb + kb) * 4) : W8_OOB;
-        rsc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rss[s_op], (int)o, 0, 0));
     };
+    const int st_u = 2 * (tid & 3), st_sw = (ld_row >> 1) & 7;
+    const int st_a0 = ld_row * 128 + 16 * (st_u ^ st_sw), st_a1 = ld_row * 128 + 16 * ((st_u + 1) ^ st_sw);
     auto store = [&](int buf) {
 #pragma unroll
         for (int op = 0; op < 2; ++op) {
+            const uint4 v = rt[op];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint32_t h[8];
 #pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                const int ch = tid + i * NT, row = ch >> 2, u = 2 * (ch & 3), sw = (row >> 1) & 7;
-                const uint4 v = rt[op][i];
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-                uint32_t h[8];
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    h[2 * d] = op == 0 ? cvt2_f16<FA>(w[d], false) : cvt2_f16<FB>(w[d], false);
-                    h[2 * d + 1] = op == 0 ? cvt2_f16<FA>(w[d], true) : cvt2_f16<FB>(w[d], true);
-                }
-                uint8_t* base = &sT[buf][op][row * 128];
-                *(uint4*)(base + 16 * (u ^ sw)) = make_uint4(h[0], h[1], h[2], h[3]);
-                *(uint4*)(base + 16 * ((u + 1) ^ sw)) = make_uint4(h[4], h[5], h[6], h[7]);
+            for (int d = 0; d < 4; ++d) {
+                h[2 * d] = op == 0 ? cvt2_f16<FA>(w[d], false) : cvt2_f16<FB>(w[d], false);
+                h[2 * d + 1] = op == 0 ? cvt2_f16<FA>(w[d], true) : cvt2_f16<FB>(w[d], true);
             }
+            *(uint4*)&sT[buf][op][st_a0] = make_uint4(h[0], h[1], h[2], h[3]);
+            *(uint4*)&sT[buf][op][st_a1] = make_uint4(h[4], h[5], h[6], h[7]);
         }
         sS[buf][s_op][s_w] = rsc;
     };
@@ -300,55 +329,83 @@ __global__ __launch_bounds__(512) void w8_f16_kernel(
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int frow = lane & 15, g = lane >> 4, fsw = (frow >> 1) & 7;
-    auto frag = [&](int buf, int op, int row, int q) -> f16x8 {
-        return *(const f16x8*)&sT[buf][op][row * 128 + 16 * ((4 * q + g) ^ fsw)];
-    };
+    const int fa_off[2] = {(wm * WTM + frow) * 128 + 16 * (g ^ fsw), (wm * WTM + frow) * 128 + 16 * ((4 + g) ^ fsw)};
+    const int fb_off[2] = {(wn * WTN + frow) * 128 + 16 * (g ^ fsw), (wn * WTN + frow) * 128 + 16 * ((4 + g) ^ fsw)};
+    const int sal_off = (wm * WTM + 16 * (frow >> 2) + 4 * g + (frow & 3)) * 2, sb_off = (wn * WTN + frow) * 2;
 
-    // K step t; MORE: step t + 1 exists, so its tile is loaded during this step and stored after it.
-    // The steady state runs with MORE constant, without branches around the loads and LDS writes.
-    auto step = [&](int t, auto more_c) {
+    // K step t (LDS buffer BUF); MORE: tile t + 1 exists, so it is loaded during this step and
+    // decoded into the other buffer after it.
+    auto step = [&](int t, auto buf_c, auto more_c) {
+        constexpr int BUF = decltype(buf_c)::value;
         constexpr bool MORE = decltype(more_c)::value;
-        const int buf = t & 1;
         if constexpr (MORE) load((t + 1) * KS);
-        f16x8 bf[TJ][2];
+        f16x8 bf[TJ][2], af[TI][2];
+        float2 sbv[TJ];
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int q = 0; q < 2; ++q) bf[j][q] = frag(buf, 1, wn * WTN + j * 16 + frow, q);
-        float2 sbv[TJ];
+            for (int q = 0; q < 2; ++q) bf[j][q] = *(const f16x8*)&sT[BUF][1][fb_off[q] + j * 16 * 128];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) sbv[j] = *(const float2*)&sS[buf][1][(wn * WTN + j * 16 + frow) * 2];
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) af[i][q] = *(const f16x8*)&sT[BUF][0][fa_off[q] + i * 16 * 128];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) sbv[j] = *(const float2*)&sS[BUF][1][sb_off + j * 32];
+        const float2 sal = *(const float2*)&sS[BUF][0][sal_off];
+        f32x4 p[2][2][TJ];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                p[0][q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][q], bf[j][q], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-            f16x8 af[2];
+            const int cb = i & 1;
 #pragma unroll
-            for (int q = 0; q < 2; ++q) af[q] = frag(buf, 0, wm * WTM + i * 16 + frow, q);
-            float2 sav[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sav[r] = *(const float2*)&sS[buf][0][(wm * WTM + i * 16 + 4 * g + r) * 2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {
-                    const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q], bf[j][q], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    const float sbq = q == 0 ? sbv[j].x : sbv[j].y;
+                    if (q == 0 && j == 0 && i + 2 < TI) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float saq = q == 0 ? sav[r].x : sav[r].y;
-                        acc[i][j][r] = fmaf(p[r], saq * sbq, acc[i][j][r]);
+                        for (int qq = 0; qq < 2; ++qq)
+                            af[i + 2 < TI ? i + 2 : i][qq] = *(const f16x8*)&sT[BUF][0][fa_off[qq] + (i + 2) * 16 * 128];
                     }
+                    if (i + 1 < TI)
+                        p[cb ^ 1][q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i + 1 < TI ? i + 1 : i][q], bf[j][q],
+                                                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const float sbq = q == 0 ? sbv[j].x : sbv[j].y;
+                    float sc[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sc[r] = w8_mul_bcast(q == 0 ? sal.x : sal.y, sbq, 4 * i + r);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[cb][q][j][r], sc[r], acc[i][j][r]);
+                    // keep the multiply-adds in this group (the compiler would sink them to their
+                    // next use, a step later)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(acc[i][j][r]));
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            }
         }
-        if constexpr (MORE) store(buf ^ 1);
+        if constexpr (MORE) store(BUF ^ 1);
         __syncthreads();
     };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
     load(0);
     store(0);
     __syncthreads();
     int t = 0;
-    for (; t + 1 < ntile; ++t) step(t, std::true_type{});
-    step(t, std::false_type{});
+    for (; t + 2 < ntile; t += 2) {
+        step(t, B0{}, std::true_type{});
+        step(t + 1, B1{}, std::true_type{});
+    }
+    if (t + 1 < ntile) {
+        step(t, B0{}, std::true_type{});
+        step(t + 1, B1{}, std::false_type{});
+    } else {
+        step(t, B0{}, std::false_type{});
+    }
     w8_store<TI, TJ, WTM, WTN, false, W8_BLOCK>(acc, sa, sb, bias, c, M, N, m0, n0, wm, wn, lane);
 }
 
