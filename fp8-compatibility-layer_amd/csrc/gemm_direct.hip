@@ -388,14 +388,14 @@ constexpr GdCfg GD_CFGS[] = {
     {64, 256, 2, 4, 6},    // 4: M <= 64, 8 waves of 32 x 64
     {32, 256, 1, 4, 7},    // 5: M <= 32, 4 waves of 32 x 64
     {128, 128, 2, 4, 6},   // 6: 8 waves of 64 x 32
-    {64, 128, 2, 2, 7},    // 7: 4 waves of 32 x 64
+    {64, 128, 2, 2, 5},    // 7: 4 waves of 32 x 64 (5 stages: 24.7 vs 25.7 us with 7 at C3 M=64)
 };
 constexpr int GD_NCFG = (int)(sizeof(GD_CFGS) / sizeof(GD_CFGS[0]));
 
 // Smallest M this kernel takes; the weight-streaming kernel serves fewer rows.  Same-box sweep on
 // MI355X at K = N = 8192, per-channel scales (us, weight-streaming vs this kernel's default
 // configuration): M=24 20.2 vs 22.5, M=32 20.9 vs 23.4, M=48 25.3 vs 24.9, M=64 27.6 vs 25.4
-// (64 x 128, 7 stages); M=128 43.4 vs 33.3 (128 x 128, 6 stages); M=256 56.1 (LDS-tiled) vs 51
+// (64 x 128, 7 stages; 24.7 with the 5 stages now used); M=128 43.4 vs 33.3 (128 x 128, 6 stages); M=256 56.1 (LDS-tiled) vs 51
 // (128 x 256, 4 stages).
 int gd_min_m() { return tune(TUNE_GEMM_DIRECT_MIN_M); }
 
@@ -485,7 +485,7 @@ static void gd_launch(int slices, int slice_len, size_t dyn, const void* x, cons
         GD_K(128, 256, 2, 4, 5)
         GD_K(64, 256, 2, 4, 6)
         GD_K(32, 256, 1, 4, 7)
-        GD_K(64, 128, 2, 2, 7)
+        GD_K(64, 128, 2, 2, 5)
     }
 #undef GD_K
 }
