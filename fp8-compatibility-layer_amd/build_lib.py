@@ -24,9 +24,15 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", os.path.j
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
 
 
+# Per-source additions.  gemv_quad.hip reads its 4x4x4 MFMA results with VALU ops every chunk; in
+# the accumulator-register form the compiler gave each chunk's result its own AGPRs (up to 128 of
+# them, and a v_accvgpr_read per value), so its MFMAs are built in the VGPR form.
+FILE_FLAGS = {"gemv_quad.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that noise.
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)

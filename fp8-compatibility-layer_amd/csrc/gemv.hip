@@ -13,6 +13,8 @@ void run_gemv_f32(const void*, int, int, const uint8_t*, int, const void*, int, 
 
 int run_gemv_pair(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
                   int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
+int run_gemv_quad(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
+                  int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
 int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, const uint8_t* w, int N, const void* ws,
                   int ws_kind, int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s);
 
@@ -23,6 +25,10 @@ int gemv_mfma_min_m() { return tune(TUNE_GEMV_MFMA_MIN); }
 
 int run_gemv(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind, int G,
              int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
+    {
+        const int rc = run_gemv_quad(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
+        if (rc != NOT_TAKEN) return rc;
+    }
     {
         const int rc = run_gemv_pair(x, x_dtype, M, K, w, N, ws, ws_kind, G, fmt, bias, y, y_dtype, s);
         if (rc != NOT_TAKEN) return rc;

@@ -35,7 +35,7 @@ void clear_error();
 enum Tune {
     TUNE_GEMV_CFG, TUNE_GEMV_WPC, TUNE_GEMV_MFMA_MIN, TUNE_GEMV_MFMA_MAX_M, TUNE_GM_NT, TUNE_GM_W, TUNE_GM_D,
     TUNE_GM_TL, TUNE_GEMM_TILE, TUNE_GEMM_SPLITK, TUNE_GEMM_DIRECT, TUNE_GEMM_DIRECT_MIN_M, TUNE_GEMM_DCFG,
-    TUNE_GS_NW, TUNE_GS_KCS, TUNE_GS_SPLITK, TUNE_GS_TL, TUNE_GEMM_V1, TUNE_GEMV_PAIR, TUNE_GEMV_PAIR_MAX_M, TUNE_COUNT
+    TUNE_GS_NW, TUNE_GS_KCS, TUNE_GS_SPLITK, TUNE_GS_TL, TUNE_GEMM_V1, TUNE_GEMV_PAIR, TUNE_GEMV_PAIR_MAX_M, TUNE_GEMV_QUAD, TUNE_GEMV_QUAD_MIN_M, TUNE_COUNT
 };
 int tune(Tune k);
 

@@ -105,9 +105,10 @@ int tfp8_dequant(const uint8_t* w, int N, int K, const void* ws, int ws_kind, in
  *   bias  [N] f32 or NULL
  *   y     [M,N] row-major, y_dtype
  *
- * M <= 8 runs the GEMV path: the row-pair GEMV for 1-4 f16/bf16 rows when K is 2048, 4096 or
- * 8192, G == K or G is 64, 128 or 256 (not 64 at K = 8192), and N is even for M > 1; otherwise
- * the streaming GEMV up to 3 rows and the matrix-core decode kernel from 4.  M > 8 runs the MFMA
+ * M <= 8 runs the GEMV path: the 4x4x4-MFMA GEMV for 3-8 f16/bf16 rows with one scale per row
+ * and K = 2048 or 4096; the row-pair GEMV for 1-4 f16/bf16 rows when K is 2048, 4096 or 8192,
+ * G == K or G is 64, 128 or 256 (not 64 at K = 8192), and N is even for M > 1; otherwise the
+ * streaming GEMV up to 3 rows and the matrix-core decode kernel from 4.  M > 8 runs the MFMA
  * GEMM path (the decode kernel up to 16 rows, then the weight-streaming, direct-to-LDS or
  * LDS-tiled GEMM by M and scale layout), which additionally needs G == K or G % 32 == 0.  fp32 activations on the GEMM path are first converted to
  * fp16 with a power-of-two row scale (tfp8_prepare_activations) in the workspace; the GEMM
@@ -160,9 +161,9 @@ int tfp8_gemm_prepared(const void* x16, int x16_dtype, const float* xs, int M, i
  * TFP8_GEMV_CFG, TFP8_GEMV_WPC, TFP8_GEMV_MFMA_MIN, TFP8_GEMV_MFMA_MAX_M, TFP8_GM_NT, TFP8_GM_W,
  * TFP8_GM_D, TFP8_GM_TL, TFP8_GEMM_TILE, TFP8_GEMM_SPLITK, TFP8_GEMM_DIRECT, TFP8_GEMM_DIRECT_MIN_M,
  * TFP8_GEMM_DCFG, TFP8_GS_NW, TFP8_GS_KCS, TFP8_GS_SPLITK, TFP8_GS_TL, TFP8_GEMM_V1, TFP8_GEMV_PAIR,
- * TFP8_GEMV_PAIR_MAX_M.  Each starts at the value of the environment variable of that name when
- * the library is loaded (or its default), and changes only through tfp8_tuning_set; the launch
- * path never reads the environment.  A knob
+ * TFP8_GEMV_PAIR_MAX_M, TFP8_GEMV_QUAD, TFP8_GEMV_QUAD_MIN_M.  Each starts at the value of the
+ * environment variable of that name when the library is loaded (or its default), and changes only
+ * through tfp8_tuning_set; the launch path never reads the environment.  A knob
  * changes routing and workspace sizes for every later call in the process: size workspaces after
  * setting knobs.  tfp8_tuning_reset restores the values read at load.  Unknown names give
  * TFP8_ERR_ARG.

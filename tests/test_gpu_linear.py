@@ -69,9 +69,9 @@ def test_kernel_switch_points_and_tails():
 
 
 def test_streaming_gemv_m1_where_pair_applies(tune):
-    """M <= 3 shapes the row-pair GEMV would take, forced through the streaming GEMV instead (and
-    M = 4 through the matrix-core decode kernel)."""
-    tune(TFP8_GEMV_PAIR=0)
+    """M <= 3 shapes the row-pair (and 4x4x4-MFMA) GEMV would take, forced through the streaming
+    GEMV instead (and M = 4 through the matrix-core decode kernel)."""
+    tune(TFP8_GEMV_PAIR=0, TFP8_GEMV_QUAD=0)
     for M in (1, 2, 3, 4):
         for N, K, G in ((14336, 4096, 128), (4096, 4096, None), (998, 2048, 64)):
             _run(M, N, K, G, torch.bfloat16, seed=N + K + M)
@@ -422,7 +422,7 @@ def test_decode_mfma_every_config(nt, w, d, tune):
     M = 1: rows past N in the last block, a K tail that is not a whole 64-byte chunk, K ranges that
     leave some waves without work, per-channel / f32 K-group (G=64) / UE8M0 K-group (G=32) scales,
     both formats, f16 and bf16 activations, with and without bias."""
-    tune(TFP8_GEMV_MFMA_MIN=1, TFP8_GEMV_PAIR=0)
+    tune(TFP8_GEMV_MFMA_MIN=1, TFP8_GEMV_PAIR=0, TFP8_GEMV_QUAD=0)
     tune(TFP8_GM_NT=nt)
     tune(TFP8_GM_W=w)
     tune(TFP8_GM_D=d)
@@ -445,7 +445,7 @@ def test_row_pair_gemv_shapes(wpb, tune):
     inside its lane segment) scales in f32 and UE8M0, both formats, f16/bf16 activations, every
     output dtype, with and without bias, M = 3 on the 4-row kernel, N odd (a half pair at the end
     at M = 1; not taken at M > 1) and below one block."""
-    tune(TFP8_GEMV_PAIR=wpb)
+    tune(TFP8_GEMV_PAIR=wpb, TFP8_GEMV_QUAD=0)
     for i, (M, N, K, G, fmt, sf, xdt, out, bias) in enumerate([
             (2, 14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
             (3, 1000, 2048, 64, "e5m2", "ue8m0", torch.float16, torch.float32, True),
@@ -465,6 +465,45 @@ def test_row_pair_gemv_shapes(wpb, tune):
         _run(1, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=wpb * 100 + i)
 
 
+def test_quad_gemv_shapes(tune):
+    """The 4x4x4-MFMA GEMV, forced for every scale layout it can take and from M = 1: one scale per
+    row and K-groups of 64/128/256 (group scales fetched across lanes), f32 and UE8M0 scales, both
+    formats, f16/bf16 activations, every output dtype, with and without bias; one or two sets of
+    four activation rows (rows past M read zeros), N not a multiple of 4 and below one block, K =
+    2048 and 4096."""
+    tune(TFP8_GEMV_QUAD=2, TFP8_GEMV_QUAD_MIN_M=1)
+    for i, (M, N, K, G, fmt, sf, xdt, out, bias) in enumerate([
+            (1, 4096, 4096, None, "e4m3fn", "f32", torch.float16, torch.float16, False),
+            (2, 14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
+            (3, 1001, 2048, 64, "e5m2", "ue8m0", torch.float16, torch.float32, True),
+            (4, 4096, 4096, None, "e4m3fn", "f32", torch.float16, torch.float16, True),
+            (5, 998, 4096, 256, "e5m2", "f32", torch.bfloat16, torch.float32, True),
+            (6, 514, 2048, 128, "e4m3fn", "ue8m0", torch.float16, torch.float16, True),
+            (7, 4102, 4096, None, "e5m2", "ue8m0", torch.bfloat16, torch.bfloat16, True),
+            (8, 14336, 4096, 128, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),
+            (8, 13, 2048, None, "e4m3fn", "f32", torch.float16, torch.float32, True),
+            (4, 7, 4096, 64, "e5m2", "f32", torch.bfloat16, torch.float16, False)]):
+        _run(M, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=3000 + i)
+
+
+def test_quad_gemv_default_routing_matches_other_kernels(tune):
+    """With the default knobs the 4x4x4-MFMA GEMV takes one-scale-per-row shapes from M = 3; the same
+    products through the row-pair GEMV (M = 3, 4) and the matrix-core decode kernel (M = 5..8) agree
+    with it to a few f32 ulps (only the summation order differs), and all are within the oracle
+    tolerance."""
+    q, s, G, b = _layer(4100, 4096, None, "e4m3fn", "f32", True, seed=31)
+    for M in (3, 4, 6, 8):
+        x = torch.randn(M, 4096, generator=torch.Generator().manual_seed(32 + M)).half().cuda()
+        outs = []
+        for quad in (1, 0):
+            tune(TFP8_GEMV_QUAD=quad)
+            outs.append(_ext.w8a16(x, q, None, s, b, torch.float32, G, "e4m3fn"))
+        torch.cuda.synchronize()
+        for y in outs:
+            _check(y, x, q, s, G, "e4m3fn", b, torch.float32, "gemv", f"quad routing M={M}")
+        assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-5), M
+
+
 def test_row_pair_gemv_matches_streaming_gemv(tune):
     """The same M = 1 products through the row-pair GEMV and the streaming GEMV (which the pair
     kernel replaced for these shapes): both within the oracle tolerance and within a few f32
@@ -474,7 +513,7 @@ def test_row_pair_gemv_matches_streaming_gemv(tune):
     x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(6)).bfloat16().cuda()
     outs = []
     for pair in (0, 1):
-        tune(TFP8_GEMV_PAIR=pair)
+        tune(TFP8_GEMV_PAIR=pair, TFP8_GEMV_QUAD=0)
         outs.append(_ext.w8a16(x, q, None, s, b, torch.float32, G, "e4m3fn"))
     torch.cuda.synchronize()
     for y in outs:
@@ -517,7 +556,7 @@ def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, tune):
     LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
     64 bytes per load): the outputs must be bit-identical."""
     print(f"[linear] decode transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
-    tune(TFP8_GEMV_PAIR=0)
+    tune(TFP8_GEMV_PAIR=0, TFP8_GEMV_QUAD=0)
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).bfloat16().cuda()
     outs = []
