@@ -81,7 +81,9 @@ __device__ __forceinline__ typename GdOp<T>::V gd_decode(uint32_t lo, uint32_t h
 // otherwise wait for every load in flight before each LDS read; the kernel orders them itself
 // (gd_wait_vm before the barrier that publishes a stage).
 // The per-lane offset voff stays in one register for the whole K loop (the K position is the
-// scalar soff), so no register a load still reads is ever overwritten.
+// scalar soff), so no register a load still reads is ever overwritten.  m0 is a register the
+// compiler reserves (hipcc warns about the clobber); these kernels give it no other use, which
+// tests/test_isa_checks.py verifies on the generated code.
 __device__ __forceinline__ void gd_load_lds(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
                  "s"(soff)
