@@ -1,5 +1,8 @@
-// GEMV entry: validated by the caller (linear.hip), 1 <= M <= 8; dispatch by activation dtype.
-// The kernel and its launch configurations are in gemv_impl.h.
+// GEMV entry: validated by the caller (linear.hip), 1 <= M <= 8.  In order of preference: the
+// 4x4x4-MFMA GEMV (gemv_quad.hip), the row-pair GEMV (gemv_pair.hip), the matrix-core decode kernel
+// (gemv_mfma.hip, from TFP8_GEMV_MFMA_MIN rows), and the streaming GEMV (gemv_impl.h, dispatched
+// by activation dtype), each taking the shapes it was measured best on and returning NOT_TAKEN
+// otherwise.
 #include "tfp8_common.h"
 
 namespace tfp8 {
