@@ -153,20 +153,28 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         (void*)(w + (size_t)n0 * K), (short)0, (int)((uint32_t)min(BN, N - n0) * (uint32_t)K), (int)GD_BUF_FLAGS);
 
     // K-group scales of the block's rows for the groups its K slice touches, staged in LDS once
-    // (UE8M0 bytes for folding, f32 values for the partial sums) before any ring load is issued.
+    // (UE8M0 bytes for folding, f32 values for the partial sums).  Up to GD_SPT per thread (every
+    // default shape), the loads go out together right before the first ring stages and are waited
+    // for with them, so their latency overlaps the ring's; more than that, the staging loop runs
+    // first, before any ring load is issued.
     extern __shared__ __attribute__((aligned(16))) uint8_t gd_scales[];
     const int gfirst = SMODE == GD_CHANNEL ? 0 : kbeg / G;
     const int nsg = SMODE == GD_CHANNEL ? 0 : (kbeg + nst * GD_BK - 1) / G - gfirst + 1;
+    constexpr int GD_SPT = 16, TPR = NW * 64 / BN;   // scales per thread; threads per weight row
+    static_assert(TPR >= 1 && TPR * BN == NW * 64, "whole threads per weight row");
+    const bool scales_early = SMODE != GD_CHANNEL && nsg > GD_SPT * TPR;
+    const int ng = SMODE == GD_CHANNEL ? 1 : K / G;
     if constexpr (SMODE != GD_CHANNEL) {
-        const int ng = K / G;
-        for (int i = tid; i < BN * nsg; i += NW * 64) {
-            const int r = i / nsg, n = min(n0 + r, N - 1);
-            const size_t src = (size_t)n * ng + gfirst + (i - r * nsg);
-            if constexpr (SMODE == GD_FOLD) gd_scales[i] = ((const uint8_t*)ws)[src];
-            else ((float*)gd_scales)[i] = sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[src])
-                                                                : ((const float*)ws)[src];
+        if (scales_early) {
+            for (int i = tid; i < BN * nsg; i += NW * 64) {
+                const int r = i / nsg, n = min(n0 + r, N - 1);
+                const size_t src = (size_t)n * ng + gfirst + (i - r * nsg);
+                if constexpr (SMODE == GD_FOLD) gd_scales[i] = ((const uint8_t*)ws)[src];
+                else ((float*)gd_scales)[i] = sk == TFP8_SCALE_UE8M0 ? ue8m0_to_f32(((const uint8_t*)ws)[src])
+                                                                    : ((const float*)ws)[src];
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
 
     // LDS layouts (16-byte units): activation row r (128 B) keeps chunk c at c ^ ((r >> 1) & 7),
@@ -294,7 +302,43 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     // (the same barrier retires step t-1's buffer, into which step t+S-1 is then issued), and both
     // K windows of step t+1 are read from LDS while step t multiplies: two register sets, swapped
     // by unrolling the loop by two.
-    for (int st = 0; st < S - 1 && st < nst; ++st) issue(st);
+    if constexpr (SMODE != GD_CHANNEL) {
+        if (!scales_early) {
+            // Thread tid stages entries j = q, q + TPR, ... (j < nsg) of row r.  The loads are inline
+            // assembly like the ring's, so the compiler adds no wait of its own for them; the
+            // explicit wait below retires them (they are older than every ring load) and the empty
+            // asm statements keep every use of the values after it.
+            const int r = tid / TPR, q = tid % TPR, n = min(n0 + r, N - 1);
+            const bool f32s = SMODE == GD_PARTIAL && sk != TFP8_SCALE_UE8M0;
+            const uint32_t esz = f32s ? 4u : 1u;
+            const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)ws, (short)0, (int)((uint32_t)N * (uint32_t)ng * esz), (int)GD_BUF_FLAGS);
+            uint32_t sv[GD_SPT];
+#pragma unroll
+            for (int u = 0; u < GD_SPT; ++u) {
+                const int j = min(q + TPR * u, nsg - 1);
+                const uint32_t off = ((uint32_t)n * (uint32_t)ng + (uint32_t)(gfirst + j)) * esz;
+                if (f32s) asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(sv[u]) : "v"(off), "s"(rsc) : "memory");
+                else asm volatile("buffer_load_ubyte %0, %1, %2, 0 offen" : "=v"(sv[u]) : "v"(off), "s"(rsc) : "memory");
+            }
+            for (int st = 0; st < S - 1 && st < nst; ++st) issue(st);
+            gd_wait_vm<LA + LB>(min(S - 1, nst));
+#pragma unroll
+            for (int u = 0; u < GD_SPT; ++u) {
+                asm volatile("" : "+v"(sv[u]));
+                const int j = q + TPR * u;
+                if (j < nsg) {
+                    if constexpr (SMODE == GD_FOLD) gd_scales[r * nsg + j] = (uint8_t)sv[u];
+                    else ((float*)gd_scales)[r * nsg + j] = f32s ? __builtin_bit_cast(float, sv[u]) : ue8m0_to_f32(sv[u]);
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // published by sync_stage's barrier
+        } else {
+            for (int st = 0; st < S - 1 && st < nst; ++st) issue(st);
+        }
+    } else {
+        for (int st = 0; st < S - 1 && st < nst; ++st) issue(st);
+    }
     Frag f0, f1, g0, g1;
     sync_stage(0, min(nst - 1, S - 2));
     read(0, 0, f0);
@@ -450,6 +494,7 @@ static bool gd_plan(int M, int N, int K, int G, int ws_kind, int x16_dtype, int*
         const bool dflt = (c.bm == 128 && c.bn == 256 && c.wm == 2 && c.wn == 4 && c.stages == 4) ||
                           (c.bm == 128 && c.bn == 128 && c.wm == 2 && c.wn == 4 && c.stages == 6);
         if (!dflt) return false;
+        if ((size_t)N * (size_t)(K / G) * 4 >= (1ull << 31)) return false;   // scale buffer resource range
         const size_t groups = (size_t)(*slice_len / G + 2);   // groups one slice can touch
         *dyn = (c.bn * groups * (md == GD_FOLD ? 1 : 4) + 15) / 16 * 16;
     }
