@@ -238,7 +238,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     struct Frag {
         V a[TM][2];
         uint4 b[TN];
-        float s[SMODE == GD_FOLD ? TN : 1];   // folded UE8M0 scale of the window's group, per tile
+        uint32_t s[SMODE == GD_FOLD ? TN : 1];   // UE8M0 byte of the window's group, per tile; fix()
+                                                 // turns it into the f32 scale's bits
     };
     auto read = [&](int st, int p, Frag& f) {
         const uint8_t* base = smem + (st % S) * STAGE;
@@ -252,7 +253,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
             // G % 32 == 0: the window's 32 codes (both lane halves) lie in one group
             const int g = (kbeg + st * GD_BK + 32 * p) / G - gfirst;
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) f.s[tn] = ue8m0_to_f32(gd_scales[scale_row(tn) + g]);
+            for (int tn = 0; tn < TN; ++tn) f.s[tn] = gd_scales[scale_row(tn) + g];
+        }
+    };
+    // The scale bytes are converted at the end of the step that read them, after its MFMAs: the
+    // wait for the byte then costs nothing, where converting it in read() would wait for the
+    // fragment reads issued just before it.
+    auto fix = [&](Frag& f) {
+        if constexpr (SMODE == GD_FOLD) {
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) f.s[tn] = __float_as_uint(ue8m0_to_f32(f.s[tn]));
         }
     };
     auto mma = [&](const Frag& f) {
@@ -260,7 +270,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                const float sc = SMODE == GD_FOLD ? f.s[SMODE == GD_FOLD ? tn : 0] : 1.f;
+                const float sc = SMODE == GD_FOLD ? __uint_as_float(f.s[SMODE == GD_FOLD ? tn : 0]) : 1.f;
                 const V bq = q ? gd_decode<T, FMT>(f.b[tn].z, f.b[tn].w, sc) : gd_decode<T, FMT>(f.b[tn].x, f.b[tn].y, sc);
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm) {
@@ -343,6 +353,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     sync_stage(0, min(nst - 1, S - 2));
     read(0, 0, f0);
     read(0, 1, f1);
+    fix(f0);
+    fix(f1);
     auto step = [&](int t, Frag& c0, Frag& c1, Frag& n0, Frag& n1) {
         const bool more = t + 1 < nst;
         if (more) sync_stage(t + 1, min(nst - 1, t + S - 2));
@@ -352,6 +364,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         if (more) read(t + 1, 1, n1);
         mma(c1);
         fold_group(t);
+        if (more) {
+            fix(n0);
+            fix(n1);
+        }
     };
     // Steady state, t + S - 1 < nst: every step issues a stage and reads the next fragments, so the
     // body has no branches and the wait counts are constants.  (With the conditional form above in
@@ -371,6 +387,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         __builtin_amdgcn_sched_barrier(0);
         mma(c1);
         fold_group(t);
+        fix(n0);
+        fix(n1);
     };
     int t = 0;
     for (; t + 1 < nst - (S - 1); t += 2) {

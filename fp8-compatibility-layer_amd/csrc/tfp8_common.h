@@ -159,9 +159,10 @@ __device__ __forceinline__ void store_elem(void* p, size_t i, int dt, float v) {
 
 // ------------------------------------------------------------------ scales
 // UE8M0 byte -> 2^(b-127); 255 is NaN (fp8_gemm_kernel.cu:22-30 rule), 0 is the subnormal 2^-127.
+// Branch-free: e << 23 is the normal value (and 0x7F800000 for 255); e = 0 and e = 255 (the two
+// bytes whose (e + 1) & 0xFF is at most 1) also set bit 22, giving 0x00400000 and 0x7FC00000.
 __device__ __forceinline__ float ue8m0_to_f32(uint32_t e) {
-    return e == 255u ? __uint_as_float(0x7FC00000u)
-                     : (e == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23));
+    return __uint_as_float((e << 23) | (((e + 1u) & 0xFFu) <= 1u ? 0x00400000u : 0u));
 }
 
 template <int SK>
