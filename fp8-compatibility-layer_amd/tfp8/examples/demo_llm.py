@@ -7,8 +7,11 @@ The model is built here (random N(0, 0.02) init, tied embedding / output head), 
 prepare_model(profile="llm_safe"), and measured the way the reference demo measures it: logits
 agreement with the bf16 model (cosine, relative L2, top-1), prefill and per-token decode latency,
 and the FP8Linear path counters.  Layout choices for the GPU:
-  * the KV cache is preallocated [B, heads, max_len, head_dim] and written in place;
-  * attention runs in fp32 on contiguous operands (scores, causal mask, softmax, values);
+  * the KV cache is preallocated in fp32 and written in place, keys as [B, heads, head_dim, max_len]
+    and values as [B, heads, max_len, head_dim], so both attention products read the cache as it
+    lies (no per-step widening or transposed copy of the whole cache); the cached values are the
+    bf16 projections widened exactly, the same numbers a bf16 cache read back in fp32 holds;
+  * attention runs in fp32 (scores, causal mask, softmax, values);
   * the tied output head keeps one fp32 copy of the embedding (the reference re-widens the
     embedding to fp32 on every call, demo_llm.py:127);
   * decoding can be replayed from one captured HIP graph (GraphDecoder): the step has static
@@ -68,22 +71,21 @@ class Attention(nn.Module):
         q = _rotary(self.q_proj(x).view(B, T, self.nh, self.hd), cos, sin)
         k = _rotary(self.k_proj(x).view(B, T, self.nkv, self.hd), cos, sin)
         v = self.v_proj(x).view(B, T, self.nkv, self.hd)
-        kc, vc = cache
-        kc[:, :, start:start + T] = k.transpose(1, 2)
+        kt, vc = cache
+        kt[:, :, :, start:start + T] = k.permute(0, 2, 3, 1)
         vc[:, :, start:start + T] = v.transpose(1, 2)
         L = start + T
         rep = self.nh // self.nkv
-        keys = kc[:, :, :L].float()
-        vals = vc[:, :, :L].float()
+        keys_t, vals = kt[:, :, :, :L], vc[:, :, :L]                         # [B, Hkv, hd, L], [B, Hkv, L, hd]
         if rep > 1:
-            keys, vals = keys.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
+            keys_t, vals = keys_t.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
         qf = q.transpose(1, 2).float().contiguous()                          # [B, H, T, hd]
-        scores = torch.matmul(qf, keys.transpose(-1, -2).contiguous()) / math.sqrt(self.hd)
+        scores = torch.matmul(qf, keys_t) / math.sqrt(self.hd)
         if T > 1:
             qpos = torch.arange(start, L, device=x.device)[:, None]
             kpos = torch.arange(L, device=x.device)[None, :]
             scores = scores.masked_fill(kpos > qpos, float("-inf"))
-        o = torch.matmul(torch.softmax(scores, -1), vals.contiguous())           # [B, H, T, hd]
+        o = torch.matmul(torch.softmax(scores, -1), vals)                       # [B, H, T, hd]
         return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
 
     def forward_static(self, x, cos, sin, cache, pos, kpos):
@@ -94,17 +96,17 @@ class Attention(nn.Module):
         q = _rotary(self.q_proj(x).view(B, T, self.nh, self.hd), cos, sin)
         k = _rotary(self.k_proj(x).view(B, T, self.nkv, self.hd), cos, sin)
         v = self.v_proj(x).view(B, T, self.nkv, self.hd)
-        kc, vc = cache
-        kc.index_copy_(2, pos, k.transpose(1, 2))
-        vc.index_copy_(2, pos, v.transpose(1, 2))
+        kt, vc = cache
+        kt.index_copy_(3, pos, k.permute(0, 2, 3, 1).float())
+        vc.index_copy_(2, pos, v.transpose(1, 2).float())
         rep = self.nh // self.nkv
-        keys, vals = kc.float(), vc.float()
+        keys_t, vals = kt, vc
         if rep > 1:
-            keys, vals = keys.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
+            keys_t, vals = keys_t.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
         qf = q.transpose(1, 2).float().contiguous()                          # [B, H, 1, hd]
-        scores = torch.matmul(qf, keys.transpose(-1, -2).contiguous()) / math.sqrt(self.hd)
+        scores = torch.matmul(qf, keys_t) / math.sqrt(self.hd)
         scores = scores.masked_fill(kpos > pos, float("-inf"))
-        o = torch.matmul(torch.softmax(scores, -1), vals.contiguous())
+        o = torch.matmul(torch.softmax(scores, -1), vals)
         return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
 
 
@@ -151,11 +153,12 @@ class Llama(nn.Module):
         self._head32 = None
 
     def new_cache(self, B, max_len, zero=False):
+        """Per layer (keys [B, n_kv, head_dim, max_len], values [B, n_kv, max_len, head_dim]), fp32."""
         c, p = self.c, self.embed.weight
         hd = c["dim"] // c["n_heads"]
         new = torch.zeros if zero else torch.empty
-        return [(new(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device),
-                 new(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device)) for _ in self.layers]
+        return [(new(B, c["n_kv"], hd, max_len, dtype=torch.float32, device=p.device),
+                 new(B, c["n_kv"], max_len, hd, dtype=torch.float32, device=p.device)) for _ in self.layers]
 
     def _rope(self, start, T, device):
         hd = self.c["dim"] // self.c["n_heads"]
