@@ -1,5 +1,6 @@
 """Build libtfp8_hip.so (gfx950) from csrc/*.hip with hipcc: one object per source, in parallel,
-then one shared library next to the Python package (tfp8/libtfp8_hip.so).
+then one shared library next to the Python package (tfp8/libtfp8_hip.so).  Also builds the example
+model's fused decode ops, tfp8/examples/llm_ops.hip -> tfp8/examples/libtfp8_llm.so.
 
     python fp8-compatibility-layer_amd/build_lib.py [--jobs N]
 
@@ -16,6 +17,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "tfp8", "libtfp8_hip.so")
+EXAMPLE_SRC = os.path.join(HERE, "tfp8", "examples", "llm_ops.hip")
+EXAMPLE_OUT = os.path.join(HERE, "tfp8", "examples", "libtfp8_llm.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -42,9 +45,11 @@ def _compile(src):
 def build(jobs=None, verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
+    jobs = jobs or min(len(srcs) + 1, os.cpu_count() or 4, 8)
     with ThreadPoolExecutor(jobs) as ex:
+        example = ex.submit(_compile, EXAMPLE_SRC)
         results = list(ex.map(_compile, srcs))
+        example = example.result()
     bad = [(s, e) for s, _, rc, e in results if rc]
     for s, _, rc, e in results:
         if e.strip() and (verbose or rc):
@@ -57,6 +62,14 @@ def build(jobs=None, verbose=False):
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
+    src, obj, rc, err = example
+    if rc:
+        raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{err}")
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", EXAMPLE_OUT + ".tmp", obj],
+                       capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(EXAMPLE_OUT + ".tmp", EXAMPLE_OUT)
     return OUT
 
 

@@ -17,9 +17,13 @@ and the FP8Linear path counters.  Layout choices for the GPU:
   * decoding can be replayed from one captured HIP graph (GraphDecoder): the step has static
     shapes -- the position is a device tensor that drives the rotary angles, the KV-cache write and
     the attention mask over the whole (zero-filled) cache -- and the greedy token and the position
-    are updated on the device, so a token costs one graph launch instead of ~400 kernel launches
-    from Python.  Prefill (static shape for a given prompt length) is captured the same way for
-    the latency figure.
+    are updated on the device, so a token costs one graph launch instead of Python's kernel
+    launches.  Prefill (static shape for a given prompt length) is captured the same way for the
+    latency figure;
+  * on the GPU the decode step runs the work between the FP8 linears as fused ops (llm_ops.hip:
+    residual add + RMSNorm, rotary + cache write, split-sequence attention, SiLU * up), about 13
+    kernels per layer where the PyTorch form of the same step (decode_step(fused=False), also the
+    CPU path) launches about 60.
 """
 import argparse
 import math
@@ -179,22 +183,46 @@ class Llama(nn.Module):
             x = layer(x, cos, sin, kv, start)
         return self._head(x)
 
-    def decode_step(self, tok, cache, pos, kpos):
+    def decode_step(self, tok, cache, pos, kpos, fused=None):
         """One greedy decode step with static shapes and device-resident state (capturable in a
         HIP graph): consumes tok [B, 1] at position pos (int64 [1]), returns the logits [B, 1, V],
         writes the next greedy token into tok and advances pos.  pos must be below the cache
-        length: it indexes the cache write on the device (GraphDecoder checks it on the host)."""
+        length: it indexes the cache write on the device (GraphDecoder checks it on the host).
+        fused (default: on CUDA tensors) runs the work between the FP8 linears as the fused ops of
+        llm_ops (one kernel each); fused=False runs the same step as PyTorch ops."""
         hd = self.c["dim"] // self.c["n_heads"]
         inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=tok.device, dtype=torch.float32) * 2.0 / hd))
         ang = pos.float()[:, None] * inv[None, :]
-        cos, sin = ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
+        cos, sin = ang.cos(), ang.sin()                                     # [1, hd / 2]
         x = self.embed(tok)
-        for layer, kv in zip(self.layers, cache):
-            x = layer.forward_static(x, cos, sin, kv, pos, kpos)
-        logits = self._head(x)
+        if tok.is_cuda if fused is None else fused:
+            logits = self._decode_fused(x, cos.reshape(-1), sin.reshape(-1), cache, pos)
+        else:
+            cos, sin = cos[None, :, None, :], sin[None, :, None, :]
+            for layer, kv in zip(self.layers, cache):
+                x = layer.forward_static(x, cos, sin, kv, pos, kpos)
+            logits = self._head(x)
         tok.copy_(greedy(logits[:, -1]))
         pos.add_(1)
         return logits
+
+    def _decode_fused(self, x, cos, sin, cache, pos):
+        """The layers and the head of decode_step with llm_ops between the FP8 linears: per layer
+        residual add + RMSNorm, rotary + cache write, attention, residual add + RMSNorm, SiLU * up
+        (the block's residual adds ride in the next norm)."""
+        from tfp8.examples import llm_ops as ops
+        H, Hkv = self.c["n_heads"], self.c["n_kv"]
+        r = None
+        for layer, (kt, vc) in zip(self.layers, cache):
+            at, mlp, n1, n2 = layer.self_attn, layer.mlp, layer.input_layernorm, layer.post_attention_layernorm
+            x, y = ops.add_rmsnorm(x, r, n1.weight, n1.eps)
+            qf = ops.rope_cache(at.q_proj(y), at.k_proj(y), at.v_proj(y), cos, sin, kt, vc, pos, H, Hkv)
+            x, y = ops.add_rmsnorm(x, at.o_proj(ops.attention(qf, kt, vc, pos, H, Hkv)), n2.weight, n2.eps)
+            r = mlp.down_proj(ops.silu_mul(mlp.gate_proj(y), mlp.up_proj(y)))
+        _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
+        if self._head32 is None or self._head32.device != y.device:
+            self._head32 = self.embed.weight.detach().float()
+        return F.linear(y.float(), self._head32)
 
 
 def greedy(logits):

@@ -1,0 +1,289 @@
+// Fused ops of one decoding position of the example Llama model (tfp8/examples/demo_llm.py), the
+// work between its FP8 linears: each op is one kernel where the PyTorch form of the same step runs
+// a chain of elementwise kernels (about 60 launches per layer become 6).  Every op keeps that
+// form's roundings -- bf16 results rounded where it rounds them, fp32 arithmetic in its order,
+// no contracted multiply-adds -- so the two forms differ only in the order of the fp32 sums
+// (the RMS of a row, the attention dot products and softmax sums).
+//
+// Built as libtfp8_llm.so beside the example (C ABI: device pointers, sizes, a hipStream_t passed
+// as void*); it is the example model's own code, not part of the FP8 library's interface.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16, round to nearest even (torch's conversion); NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t to_bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+// Sum / max over a 256-thread block (every thread gets the result); red holds 4 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// h = x + r (bf16 add; r null: h = x) and y = bf16((float(h) * rsqrt(mean(float(h)^2) + eps)) * float(w)),
+// the RMSNorm of demo_llm.RMSNorm.forward.  One 256-thread block per row, CH chunks of 8 elements
+// per thread (d % 8 == 0, d <= 2048 CH).
+template <int CH>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
+                                                          uint16_t* __restrict__ h, uint16_t* __restrict__ y,
+                                                          const uint16_t* __restrict__ w, int d, float eps) {
+    __shared__ float red[4];
+    const size_t base = (size_t)blockIdx.x * d;
+    float v[CH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = (c * 256 + (int)threadIdx.x) * 8;
+        if (i < d) {
+            const uint4 xa = *(const uint4*)(x + base + i);
+            const uint16_t* xs = (const uint16_t*)&xa;
+            uint4 ha = xa;
+            uint16_t* hs = (uint16_t*)&ha;
+            if (r) {
+                const uint4 ra = *(const uint4*)(r + base + i);
+                const uint16_t* rs = (const uint16_t*)&ra;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) hs[j] = to_bf(__fadd_rn(bf(xs[j]), bf(rs[j])));
+                *(uint4*)(h + base + i) = ha;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[c][j] = bf(hs[j]);
+                ss = __fadd_rn(ss, __fmul_rn(v[c][j], v[c][j]));
+            }
+        }
+    }
+    const float ms = __fdiv_rn(block_sum(ss, red), (float)d);
+    const float inv = rsqrtf(__fadd_rn(ms, eps));
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = (c * 256 + (int)threadIdx.x) * 8;
+        if (i < d) {
+            const uint4 wa = *(const uint4*)(w + i);
+            const uint16_t* ws = (const uint16_t*)&wa;
+            uint4 ya;
+            uint16_t* ys = (uint16_t*)&ya;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ys[j] = to_bf(__fmul_rn(__fmul_rn(v[c][j], inv), bf(ws[j])));
+            *(uint4*)(y + base + i) = ya;
+        }
+    }
+}
+
+// Rotary embedding of one position and the KV-cache write (demo_llm._rotary and the index_copy_ of
+// Attention.forward_static): x = [x1, x2] -> bf16([x1 c - x2 s, x2 c + x1 s]).  Block (head, b),
+// hd / 2 threads: heads below H are query heads (out: qf [B, H, hd] fp32, the rotated bf16 values
+// widened); the next Hkv are key heads, written widened into kt [B, Hkv, hd, L] at column *pos,
+// with the value head into vc [B, Hkv, L, hd] at row *pos.  A position outside the cache writes
+// nothing (the host checks it; this only keeps a bad position from writing out of bounds).
+__global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                  const uint16_t* __restrict__ v, const float* __restrict__ cs,
+                                  const float* __restrict__ sn, float* __restrict__ qf, float* __restrict__ kt,
+                                  float* __restrict__ vc, const int64_t* __restrict__ pos, int H, int Hkv, int hd,
+                                  int L) {
+    const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = hd / 2;
+    const float c = cs[i], s = sn[i];
+    if (head < H) {
+        const uint16_t* src = q + ((size_t)b * H + head) * hd;
+        const float x1 = bf(src[i]), x2 = bf(src[i + half]);
+        float* dst = qf + ((size_t)b * H + head) * hd;
+        dst[i] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
+        dst[i + half] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s))));
+        return;
+    }
+    const int64_t p = *pos;
+    if (p < 0 || p >= L) return;
+    const int kh = head - H;
+    const size_t hb = (size_t)b * Hkv + kh;
+    const uint16_t* src = k + hb * hd;
+    const float x1 = bf(src[i]), x2 = bf(src[i + half]);
+    kt[(hb * hd + i) * L + p] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
+    kt[(hb * hd + i + half) * L + p] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s))));
+    const uint16_t* vs = v + hb * hd;
+    vc[(hb * L + p) * hd + i] = bf(vs[i]);
+    vc[(hb * L + p) * hd + i + half] = bf(vs[i + half]);
+}
+
+// Decode attention over cache positions 0..*pos, split over gridDim.y chunks of at most 64
+// positions.  Block (b * H + h, j), 4 waves: lane l takes position t0 + l, wave w the dot product
+// over head dimensions [w HD/4, (w+1) HD/4) (every load of a lane in flight at once), summed over
+// the waves in LDS: s_t = (q . k_t) / sdiv.  Then m = max s_t, l = sum exp(s_t - m) and
+// o[i] = sum exp(s_t - m) v_t[i], stored as part[(bh * S + j) * (HD + 2) + {0: m, 1: l, 2 + i: o[i]}]
+// (an empty chunk stores m = -inf, l = 0, o = 0).  Query head h reads key/value head h / (H / Hkv)
+// (repeat_interleave over heads).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict__ qf, const float* __restrict__ kt,
+                                                        const float* __restrict__ vc, const int64_t* __restrict__ pos,
+                                                        float* __restrict__ part, int H, int Hkv, int L, float sdiv) {
+    constexpr int Q = HD / 4, G = 256 / HD;
+    __shared__ float qs[HD], dots[4][64], e[64], oacc[256];
+    const int bh = blockIdx.x, j = blockIdx.y, S = gridDim.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int b = bh / H, h = bh - b * H, kh = h / (H / Hkv);
+    const size_t hb = (size_t)b * Hkv + kh;
+    const int n = (int)min((int64_t)L, max((int64_t)0, *pos + 1));
+    const int chunk = (n + S - 1) / S, t0 = min(n, j * chunk), cnt = min(n, t0 + chunk) - t0;
+    if (tid < HD) qs[tid] = qf[(size_t)bh * HD + tid];
+    __syncthreads();
+    if (lane < cnt) {
+        const float* kp = kt + (hb * HD + w * Q) * L + t0 + lane;
+        float kv[Q];
+#pragma unroll
+        for (int i = 0; i < Q; ++i) kv[i] = kp[(size_t)i * L];
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < Q; ++i) dot = fmaf(qs[w * Q + i], kv[i], dot);
+        dots[w][lane] = dot;
+    }
+    __syncthreads();
+    float m = -INFINITY, l = 0.f;
+    if (w == 0) {
+        const float sv = lane < cnt ? __fdiv_rn(__fadd_rn(__fadd_rn(dots[0][lane], dots[1][lane]),
+                                                          __fadd_rn(dots[2][lane], dots[3][lane])), sdiv)
+                                    : -INFINITY;
+        m = wave_max(sv);
+        const float ev = lane < cnt ? expf(__fsub_rn(sv, m)) : 0.f;
+        e[lane] = ev;
+        l = wave_sum(ev);
+    }
+    __syncthreads();
+    // o: G groups of HD threads; group g sums positions g, g + G, ... (loads independent of the sums)
+    const int g = tid / HD, i = tid - g * HD;
+    const float* vp = vc + (hb * L + t0) * HD + i;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int t = g; t < cnt; t += G) acc = fmaf(e[t], vp[(size_t)t * HD], acc);
+    oacc[tid] = acc;
+    __syncthreads();
+    float* out = part + ((size_t)bh * S + j) * (HD + 2);
+    if (tid < HD) {
+        float o = oacc[tid];
+#pragma unroll
+        for (int gg = 1; gg < G; ++gg) o = __fadd_rn(o, oacc[gg * HD + tid]);
+        out[2 + tid] = o;
+    }
+    if (tid == 0) {
+        out[0] = cnt > 0 ? m : -INFINITY;
+        out[1] = l;
+    }
+}
+
+// Combines the chunks: o[i] = sum_j o_j[i] e^(m_j - M) / sum_j l_j e^(m_j - M), M = max_j m_j,
+// rounded to bf16 into out [B, H * hd] (the layout o_proj reads).  Block bh, 256 threads: the
+// chunks' (m, l) pairs are staged in LDS with one load each, then thread i < hd adds its column.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, uint16_t* __restrict__ out,
+                                                           int hd, int S) {
+    __shared__ float mj[256], fj[256], red[4];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const float* p = part + (size_t)bh * S * (hd + 2);
+    const float mv = tid < S ? p[(size_t)tid * (hd + 2)] : -INFINITY;
+    const float lv = tid < S ? p[(size_t)tid * (hd + 2) + 1] : 0.f;
+    const float M = block_max(mv, red);
+    const float f = mv == -INFINITY ? 0.f : expf(__fsub_rn(mv, M));
+    mj[tid] = lv;
+    fj[tid] = f;
+    __syncthreads();
+    if (tid < hd) {
+        float num = 0.f, den = 0.f;
+        for (int j = 0; j < S; ++j) {
+            num = fmaf(p[(size_t)j * (hd + 2) + 2 + tid], fj[j], num);
+            den = fmaf(mj[j], fj[j], den);
+        }
+        out[(size_t)bh * hd + tid] = to_bf(__fdiv_rn(num, den));
+    }
+}
+
+// out = bf16(bf16(silu(g)) * u), silu(x) = x / (1 + exp(-x)) in fp32 (F.silu then the product of
+// MLP.forward).
+__global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                uint16_t* __restrict__ out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = bf(g[i]);
+        const float sv = bf(to_bf(__fdiv_rn(x, __fadd_rn(1.f, expf(-x)))));
+        out[i] = to_bf(__fmul_rn(sv, bf(u[i])));
+    }
+}
+
+int launched() { return (int)hipGetLastError(); }
+
+}  // namespace
+
+extern "C" {
+
+// Error codes: 0, a hipError_t, or -1 for arguments these kernels do not take.
+int tfp8_llm_add_rmsnorm(const void* x, const void* r, void* h, void* y, const void* w, int rows, int d, float eps,
+                         void* stream) {
+    if (rows < 0 || d <= 0 || d % 8 || d > 2048 * 4 || !x || !y || !w || (r && !h)) return -1;
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)r | (uintptr_t)h) % 16) return -1;
+    if (rows == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    const uint16_t *xp = (const uint16_t*)x, *rp = (const uint16_t*)r, *wp = (const uint16_t*)w;
+    uint16_t *hp = (uint16_t*)h, *yp = (uint16_t*)y;
+    if (d <= 2048) add_rmsnorm_kernel<1><<<rows, 256, 0, s>>>(xp, rp, hp, yp, wp, d, eps);
+    else if (d <= 4096) add_rmsnorm_kernel<2><<<rows, 256, 0, s>>>(xp, rp, hp, yp, wp, d, eps);
+    else add_rmsnorm_kernel<4><<<rows, 256, 0, s>>>(xp, rp, hp, yp, wp, d, eps);
+    return launched();
+}
+
+int tfp8_llm_rope_cache(const void* q, const void* k, const void* v, const float* cs, const float* sn, float* qf,
+                        float* kt, float* vc, const int64_t* pos, int B, int H, int Hkv, int hd, int L, void* stream) {
+    if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 512 || L <= 0) return -1;
+    if (!q || !k || !v || !cs || !sn || !qf || !kt || !vc || !pos) return -1;
+    if (B == 0) return 0;
+    rope_cache_kernel<<<dim3(H + Hkv, B), hd / 2, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, qf, kt, vc, pos, H, Hkv, hd, L);
+    return launched();
+}
+
+// Chunks S with S * 64 >= L and S <= 256; head dimension 64 or 128; part holds B * H * S * (hd + 2) floats.
+int tfp8_llm_attention(const float* qf, const float* kt, const float* vc, const int64_t* pos, float* part, int S,
+                       void* out, int B, int H, int Hkv, int hd, int L, float sdiv, void* stream) {
+    if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || L <= 0) return -1;
+    if (S <= 0 || (int64_t)S * 64 < L || S > 256 || !qf || !kt || !vc || !pos || !part || !out) return -1;
+    if (B == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    if (hd == 128) attn_part_kernel<128><<<dim3(B * H, S), 256, 0, s>>>(qf, kt, vc, pos, part, H, Hkv, L, sdiv);
+    else attn_part_kernel<64><<<dim3(B * H, S), 256, 0, s>>>(qf, kt, vc, pos, part, H, Hkv, L, sdiv);
+    int rc = launched();
+    if (rc) return rc;
+    attn_combine_kernel<<<B * H, 256, 0, s>>>(part, (uint16_t*)out, hd, S);
+    return launched();
+}
+
+int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int64_t n, void* stream) {
+    if (n < 0 || !g || !u || !out) return -1;
+    if (n == 0) return 0;
+    const int64_t blocks = (n + 255) / 256;
+    silu_mul_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, n);
+    return launched();
+}
+
+}  // extern "C"

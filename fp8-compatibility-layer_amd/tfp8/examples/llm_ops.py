@@ -1,0 +1,117 @@
+"""ctypes bindings of libtfp8_llm.so, the example model's fused decode-step ops (llm_ops.hip).
+
+Each function takes CUDA tensors, checks their shapes and dtypes, launches on torch's current
+stream (so the calls record into a HIP graph under capture) and returns new output tensors.  The
+library is the example model's own code; demo_llm uses it for the decode step on the GPU and raises
+if it is missing there."""
+import ctypes
+import math
+import os
+
+import torch
+
+_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtfp8_llm.so")
+_LIB = None
+
+
+def library():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(_PATH):
+            raise RuntimeError(f"{_PATH} is not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(_PATH)
+        p, i, f, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64
+        lib.tfp8_llm_add_rmsnorm.argtypes = [p, p, p, p, p, i, i, f, p]
+        lib.tfp8_llm_rope_cache.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, p]
+        lib.tfp8_llm_attention.argtypes = [p, p, p, p, p, i, p, i, i, i, i, i, f, p]
+        lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i64, p]
+        for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul):
+            fn.restype = ctypes.c_int
+        _LIB = lib
+    return _LIB
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _check(rc, what):
+    if rc:
+        raise RuntimeError(f"{what} failed (rc={rc})")
+
+
+def _bf16(t, what):
+    if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{what}: contiguous bfloat16 CUDA tensor expected, got {t.dtype} {t.device}")
+
+
+def add_rmsnorm(x, r, weight, eps):
+    """(h, y): h = x + r (bf16; h is x when r is None), y = RMSNorm(h) with `weight` (bf16 in and out,
+    fp32 inside), over the last dimension."""
+    _bf16(x, "x")
+    _bf16(weight, "weight")
+    d = x.shape[-1]
+    if weight.numel() != d:
+        raise ValueError(f"weight has {weight.numel()} elements, rows have {d}")
+    h = x
+    if r is not None:
+        _bf16(r, "r")
+        if r.shape != x.shape:
+            raise ValueError(f"x {tuple(x.shape)} and r {tuple(r.shape)} differ")
+        h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    _check(library().tfp8_llm_add_rmsnorm(x.data_ptr(), r.data_ptr() if r is not None else None,
+                                          h.data_ptr() if r is not None else None, y.data_ptr(), weight.data_ptr(),
+                                          x.numel() // d, d, float(eps), _stream(x)), "add_rmsnorm")
+    return h, y
+
+
+def rope_cache(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
+    """Rotary embedding of one position's q, k (bf16 [B, 1, heads * hd]) with cos/sin (fp32 [hd / 2]),
+    k and v written (widened to fp32) into the caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at
+    position pos (int64 [1] on the device); returns the rotated q widened to fp32 [B, n_heads, hd]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _bf16(t, n)
+    B, hd, L = q.shape[0], kt.shape[2], kt.shape[3]
+    if q.numel() != B * n_heads * hd or k.numel() != B * n_kv * hd or v.numel() != k.numel():
+        raise ValueError("q/k/v sizes do not match the heads")
+    if tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
+        raise ValueError(f"cache shapes {tuple(kt.shape)} / {tuple(vc.shape)}")
+    for t, n in ((kt, "kt"), (vc, "vc"), (cos, "cos"), (sin, "sin")):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{n}: contiguous float32 expected")
+    if cos.numel() != hd // 2 or sin.numel() != hd // 2 or pos.dtype != torch.int64 or pos.numel() != 1:
+        raise ValueError("cos/sin need hd / 2 values and pos one int64")
+    qf = torch.empty(B, n_heads, hd, dtype=torch.float32, device=q.device)
+    _check(library().tfp8_llm_rope_cache(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                         qf.data_ptr(), kt.data_ptr(), vc.data_ptr(), pos.data_ptr(), B, n_heads, n_kv,
+                                         hd, L, _stream(q)), "rope_cache")
+    return qf
+
+
+def attention(qf, kt, vc, pos, n_heads, n_kv):
+    """softmax((q . k_t) / sqrt(hd), t <= pos) weighted sum of v_t for every (batch, head), over the
+    caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] (fp32); returns bf16 [B, 1, n_heads * hd]."""
+    B, hd, L = qf.shape[0], kt.shape[2], kt.shape[3]
+    if tuple(qf.shape) != (B, n_heads, hd) or qf.dtype != torch.float32 or not qf.is_contiguous():
+        raise ValueError(f"qf {tuple(qf.shape)} {qf.dtype}")
+    S = math.ceil(L / 64)                          # chunks of at most 64 positions (one per lane)
+    if S > 256:
+        raise ValueError(f"cache of {L} positions: at most {256 * 64}")
+    part = torch.empty(B * n_heads * S * (hd + 2), dtype=torch.float32, device=qf.device)
+    out = torch.empty(B, 1, n_heads * hd, dtype=torch.bfloat16, device=qf.device)
+    _check(library().tfp8_llm_attention(qf.data_ptr(), kt.data_ptr(), vc.data_ptr(), pos.data_ptr(), part.data_ptr(), S,
+                                        out.data_ptr(), B, n_heads, n_kv, hd, L, float(math.sqrt(hd)), _stream(qf)),
+           "attention")
+    return out
+
+
+def silu_mul(g, u):
+    """bf16(bf16(silu(g)) * u), elementwise."""
+    _bf16(g, "g")
+    _bf16(u, "u")
+    if g.shape != u.shape:
+        raise ValueError(f"g {tuple(g.shape)} and u {tuple(u.shape)} differ")
+    out = torch.empty_like(g)
+    _check(library().tfp8_llm_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(), _stream(g)), "silu_mul")
+    return out

@@ -193,3 +193,103 @@ def test_graph_decode_replays_match_eager():
     dec.tok.copy_(tok0)
     dec.step()
     assert torch.equal(dec.tok, e_toks[0]) and dec.next_pos == T + 1
+
+
+def _bf16_ulps(a, b):
+    """Distance in bf16 units in the last place between two bf16 tensors of finite values."""
+    ia, ib = a.view(torch.int16).int(), b.view(torch.int16).int()
+    ia = torch.where(ia < 0, -32768 - ia, ia)        # sign-magnitude -> monotonic integers
+    ib = torch.where(ib < 0, -32768 - ib, ib)
+    return (ia - ib).abs()
+
+
+def test_llm_ops_match_pytorch_forms():
+    """Each fused decode-step op (tfp8/examples/llm_ops.hip) against the PyTorch form it replaces in
+    the example model: the elementwise ops with the same roundings bit for bit (residual add,
+    rotary, cache write); the RMSNorm (whose fp32 row sum is ordered differently) within one bf16
+    ulp; SiLU * up within one bf16 ulp (exp); attention within bf16 rounding of the fp32 result."""
+    from tfp8.examples import llm_ops as ops
+    g = torch.Generator("cuda").manual_seed(11)
+    B, H, Hkv, hd, L, d = 3, 8, 4, 128, 300, 1024
+    print(f"[llm_ops] B={B} H={H} Hkv={Hkv} hd={hd} L={L} d={d}", flush=True)
+
+    x = torch.randn(B, 1, d, device="cuda", generator=g).bfloat16()
+    r = torch.randn(B, 1, d, device="cuda", generator=g).bfloat16()
+    norm = demo_llm.RMSNorm(d).cuda().bfloat16()
+    norm.weight.data = (1 + 0.1 * torch.randn(d, device="cuda", generator=g)).bfloat16()
+    with torch.no_grad():
+        h, y = ops.add_rmsnorm(x, r, norm.weight, norm.eps)
+        assert torch.equal(h, x + r)
+        assert _bf16_ulps(y, norm(x + r)).max().item() <= 1
+        h0, y0 = ops.add_rmsnorm(x, None, norm.weight, norm.eps)
+        assert h0 is x and _bf16_ulps(y0, norm(x)).max().item() <= 1
+
+        gg = (3 * torch.randn(B, 1, 4 * d, device="cuda", generator=g)).bfloat16()
+        uu = torch.randn(B, 1, 4 * d, device="cuda", generator=g).bfloat16()
+        assert _bf16_ulps(ops.silu_mul(gg, uu), torch.nn.functional.silu(gg) * uu).max().item() <= 1
+
+        # rotary + cache write at position p, and attention over 0..p, against the static step's
+        # PyTorch ops (Attention.forward_static with the same caches)
+        p = 217
+        pos = torch.tensor([p], dtype=torch.long, device="cuda")
+        kt = torch.randn(B, Hkv, hd, L, device="cuda", generator=g)
+        vc = torch.randn(B, Hkv, L, hd, device="cuda", generator=g)
+        kt2, vc2 = kt.clone(), vc.clone()
+        q = torch.randn(B, 1, H * hd, device="cuda", generator=g).bfloat16()
+        k = torch.randn(B, 1, Hkv * hd, device="cuda", generator=g).bfloat16()
+        v = torch.randn(B, 1, Hkv * hd, device="cuda", generator=g).bfloat16()
+        inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device="cuda", dtype=torch.float32) * 2.0 / hd))
+        ang = pos.float()[:, None] * inv[None, :]
+        cos, sin = ang.cos(), ang.sin()
+        qf = ops.rope_cache(q, k, v, cos.reshape(-1), sin.reshape(-1), kt, vc, pos, H, Hkv)
+        c4, s4 = cos[None, :, None, :], sin[None, :, None, :]
+        q_ref = demo_llm._rotary(q.view(B, 1, H, hd), c4, s4)
+        k_ref = demo_llm._rotary(k.view(B, 1, Hkv, hd), c4, s4)
+        assert torch.equal(qf, q_ref.view(B, H, hd).float())
+        kt2.index_copy_(3, pos, k_ref.permute(0, 2, 3, 1).float())
+        vc2.index_copy_(2, pos, v.view(B, 1, Hkv, hd).transpose(1, 2).float())
+        assert torch.equal(kt, kt2) and torch.equal(vc, vc2)
+
+        o = ops.attention(qf, kt, vc, pos, H, Hkv)
+        rep = H // Hkv
+        scores = torch.matmul(qf.view(B, H, 1, hd), kt.repeat_interleave(rep, 1)) / (hd ** 0.5)
+        scores = scores.masked_fill(torch.arange(L, device="cuda") > pos, float("-inf"))
+        o_ref32 = torch.matmul(torch.softmax(scores, -1), vc.repeat_interleave(rep, 1))     # [B, H, 1, hd]
+        o_ref32 = o_ref32.transpose(1, 2).reshape(B, 1, H * hd)
+        err = (o.float() - o_ref32).abs()
+        assert (err <= 2.0 ** -8 * o_ref32.abs() + 1e-5).all(), err.max().item()
+
+        # the first position (one cached row) and the last one (every row) of the cache
+        for p in (0, L - 1):
+            pos.fill_(p)
+            o = ops.attention(qf, kt, vc, pos, H, Hkv)
+            sc = torch.matmul(qf.view(B, H, 1, hd), kt.repeat_interleave(rep, 1)) / (hd ** 0.5)
+            sc = sc.masked_fill(torch.arange(L, device="cuda") > pos, float("-inf"))
+            ref = torch.matmul(torch.softmax(sc, -1), vc.repeat_interleave(rep, 1)).transpose(1, 2).reshape(B, 1, H * hd)
+            assert ((o.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-5).all(), p
+
+
+def test_fused_decode_step_matches_pytorch_step():
+    """The decode step with the fused ops between the FP8 linears against the same step as PyTorch
+    ops (decode_step(fused=False)): the same greedy tokens over 16 steps at B=1 and B=3, and logits
+    within the bf16 rounding noise of the step (relative L2 below 1e-2, cosine above 0.9999)."""
+    model = demo_llm.build("tiny")
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn"))
+    for B in (1, 3):
+        T, NEW = 20, 16
+        print(f"[fused] tiny B={B} prompt {T} decode {NEW}", flush=True)
+        prompt = torch.randint(0, model.c["vocab"], (B, T), device="cuda", generator=torch.Generator("cuda").manual_seed(B))
+        runs = {}
+        with torch.no_grad():
+            for fused in (False, True):
+                dec = demo_llm.GraphDecoder(model, B, T + NEW + 2)
+                dec.prefill(prompt)
+                toks, logits = [], []
+                for _ in range(NEW):
+                    logits.append(model.decode_step(dec.tok, dec.cache, dec.pos, dec.kpos, fused=fused)[:, -1].clone())
+                    toks.append(dec.tok.clone())
+                runs[fused] = (torch.cat(toks, 1), torch.stack(logits, 1))
+        assert torch.equal(runs[True][0], runs[False][0])
+        cos, rel, top1 = demo_llm.agreement(runs[False][1], runs[True][1])
+        print(f"[fused] B={B}: cosine {cos:.7f} rel L2 {rel:.2e} top-1 {100 * top1:.1f}%", flush=True)
+        assert rel < 1e-2 and cos > 0.9999 and top1 == 1.0, (B, cos, rel, top1)

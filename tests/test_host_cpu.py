@@ -331,6 +331,25 @@ def test_abi_argument_validation_without_gpu():
     assert lib.tfp8_linear_workspace_size(2, 64, 128, 256) >= 64 * 256 * 2   # fp32 prep buffer
 
 
+def test_example_ops_library_loads_and_validates_without_gpu():
+    """libtfp8_llm.so (the example model's fused decode ops) exports its four entry points and
+    refuses arguments its kernels do not take before launching anything."""
+    from tfp8.examples import llm_ops
+    lib = llm_ops.library()
+    for n in ("tfp8_llm_add_rmsnorm", "tfp8_llm_rope_cache", "tfp8_llm_attention", "tfp8_llm_silu_mul"):
+        assert hasattr(lib, n), n
+    buf = ctypes.create_string_buffer(4096)
+    a = (ctypes.addressof(buf) + 255) & ~255
+    assert lib.tfp8_llm_add_rmsnorm(a, None, None, a, a, 1, 12, 1e-5, None) == -1        # d % 8
+    assert lib.tfp8_llm_add_rmsnorm(a + 2, None, None, a, a, 1, 16, 1e-5, None) == -1    # alignment
+    assert lib.tfp8_llm_add_rmsnorm(a, None, None, a, a, 0, 16, 1e-5, None) == 0         # no rows
+    assert lib.tfp8_llm_rope_cache(a, a, a, a, a, a, a, a, a, 1, 6, 4, 128, 64, None) == -1   # H % Hkv
+    assert lib.tfp8_llm_attention(a, a, a, a, a, 2, a, 1, 4, 4, 96, 64, 1.0, None) == -1     # head dim
+    assert lib.tfp8_llm_attention(a, a, a, a, a, 1, a, 1, 4, 4, 128, 65, 1.0, None) == -1    # S * 64 < L
+    assert lib.tfp8_llm_silu_mul(a, a, a, -1, None) == -1
+    assert lib.tfp8_llm_silu_mul(a, a, a, 0, None) == 0
+
+
 def test_available_false_and_require_raises_without_gpu():
     if torch.cuda.is_available():
         pytest.skip("GPU present")
