@@ -191,7 +191,10 @@ class Llama(nn.Module):
         fused (default: on CUDA tensors) runs the work between the FP8 linears as the fused ops of
         llm_ops (one kernel each); fused=False runs the same step as PyTorch ops."""
         hd = self.c["dim"] // self.c["n_heads"]
-        inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=tok.device, dtype=torch.float32) * 2.0 / hd))
+        inv = self.__dict__.get("_rope_inv")             # the angles' frequencies, computed once per device
+        if inv is None or inv.device != tok.device:
+            inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=tok.device, dtype=torch.float32) * 2.0 / hd))
+            self.__dict__["_rope_inv"] = inv
         ang = pos.float()[:, None] * inv[None, :]
         cos, sin = ang.cos(), ang.sin()                                     # [1, hd / 2]
         x = self.embed(tok)
@@ -206,23 +209,64 @@ class Llama(nn.Module):
         pos.add_(1)
         return logits
 
+    def _fused_projections(self):
+        """Per layer (qkv, gate_up): one FP8Linear over the rows of q/k/v_proj and one over those of
+        gate/up_proj, for the decode step -- the codes and scales are the separate layers' rows, so
+        every output is the same row product, in two GEMV launches instead of five.  None where the
+        layers are not FP8Linear of one layout.  Rebuilt when the layers or their weights change;
+        the first decode step builds them (GraphDecoder's warm-up steps, outside graph capture)."""
+        srcs = [(l.self_attn.q_proj, l.self_attn.k_proj, l.self_attn.v_proj, l.mlp.gate_proj, l.mlp.up_proj)
+                for l in self.layers]
+        key = tuple((id(m), (m.qweight if "qweight" in m._buffers else m.weight).data_ptr()) for t in srcs for m in t)
+        if self.__dict__.get("_fused_key") != key:        # kept in __dict__: not registered as submodules
+            self.__dict__["_fused_proj"] = [(_concat_fp8(t[:3]), _concat_fp8(t[3:])) for t in srcs]
+            self.__dict__["_fused_key"] = key
+        return self.__dict__["_fused_proj"]
+
     def _decode_fused(self, x, cos, sin, cache, pos):
         """The layers and the head of decode_step with llm_ops between the FP8 linears: per layer
-        residual add + RMSNorm, rotary + cache write, attention, residual add + RMSNorm, SiLU * up
-        (the block's residual adds ride in the next norm)."""
+        residual add + RMSNorm, q/k/v projection (one fused FP8Linear), rotary + cache write,
+        attention, o_proj, residual add + RMSNorm, gate/up projection (one fused FP8Linear), SiLU * up,
+        down_proj (the block's residual adds ride in the next norm)."""
         from tfp8.examples import llm_ops as ops
-        H, Hkv = self.c["n_heads"], self.c["n_kv"]
+        H, Hkv, ffn = self.c["n_heads"], self.c["n_kv"], self.c["ffn"]
+        nq, nk = self.c["dim"], Hkv * (self.c["dim"] // H)
         r = None
-        for layer, (kt, vc) in zip(self.layers, cache):
+        for layer, (kt, vc), (qkv, gate_up) in zip(self.layers, cache, self._fused_projections()):
             at, mlp, n1, n2 = layer.self_attn, layer.mlp, layer.input_layernorm, layer.post_attention_layernorm
             x, y = ops.add_rmsnorm(x, r, n1.weight, n1.eps)
-            qf = ops.rope_cache(at.q_proj(y), at.k_proj(y), at.v_proj(y), cos, sin, kt, vc, pos, H, Hkv)
+            if qkv is not None:
+                o = qkv(y)
+                q, k, v = o[..., :nq], o[..., nq:nq + nk], o[..., nq + nk:]
+            else:
+                q, k, v = at.q_proj(y), at.k_proj(y), at.v_proj(y)
+            qf = ops.rope_cache(q, k, v, cos, sin, kt, vc, pos, H, Hkv)
             x, y = ops.add_rmsnorm(x, at.o_proj(ops.attention(qf, kt, vc, pos, H, Hkv)), n2.weight, n2.eps)
-            r = mlp.down_proj(ops.silu_mul(mlp.gate_proj(y), mlp.up_proj(y)))
+            if gate_up is not None:
+                o = gate_up(y)
+                g, u = o[..., :ffn], o[..., ffn:]
+            else:
+                g, u = mlp.gate_proj(y), mlp.up_proj(y)
+            r = mlp.down_proj(ops.silu_mul(g, u))
         _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
         if self._head32 is None or self._head32.device != y.device:
             self._head32 = self.embed.weight.detach().float()
         return F.linear(y.float(), self._head32)
+
+
+def _concat_fp8(mods):
+    """One FP8Linear whose output rows are those of `mods` in order (FP8Linear layers with one input
+    size, format, group size, scale storage and output dtype, no bias, not backed off), or None."""
+    from tfp8.linear import FP8Linear
+    f0 = mods[0]
+    if not all(isinstance(f, FP8Linear) and f.fallback is None and f.bias_f32 is None
+               and (f.in_features, f.fmt, f.group_size, f.scale_format, f.out_dtype)
+               == (f0.in_features, f0.fmt, f0.group_size, f0.scale_format, f0.out_dtype) for f in mods):
+        return None
+    with torch.no_grad():
+        q = torch.cat([f.qweight for f in mods])
+        s = torch.cat([f.weight_scale for f in mods])
+    return FP8Linear.from_fp8_checkpoint(q, s, None, f0.fmt, out_dtype=f0.out_dtype, nan_check=f0.nan_check)
 
 
 def greedy(logits):

@@ -102,17 +102,18 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
 // Attention.forward_static): x = [x1, x2] -> bf16([x1 c - x2 s, x2 c + x1 s]).  Block (head, b),
 // hd / 2 threads: heads below H are query heads (out: qf [B, H, hd] fp32, the rotated bf16 values
 // widened); the next Hkv are key heads, written widened into kt [B, Hkv, hd, L] at column *pos,
-// with the value head into vc [B, Hkv, L, hd] at row *pos.  A position outside the cache writes
-// nothing (the host checks it; this only keeps a bad position from writing out of bounds).
+// with the value head into vc [B, Hkv, L, hd] at row *pos.  Row b of q / k / v starts ldq / ldk /
+// ldv elements after row b - 1 (slices of one fused projection).  A position outside the cache
+// writes nothing (the host checks it; this only keeps a bad position from writing out of bounds).
 __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                   const uint16_t* __restrict__ v, const float* __restrict__ cs,
                                   const float* __restrict__ sn, float* __restrict__ qf, float* __restrict__ kt,
                                   float* __restrict__ vc, const int64_t* __restrict__ pos, int H, int Hkv, int hd,
-                                  int L) {
+                                  int L, int ldq, int ldk, int ldv) {
     const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = hd / 2;
     const float c = cs[i], s = sn[i];
     if (head < H) {
-        const uint16_t* src = q + ((size_t)b * H + head) * hd;
+        const uint16_t* src = q + (size_t)b * ldq + (size_t)head * hd;
         const float x1 = bf(src[i]), x2 = bf(src[i + half]);
         float* dst = qf + ((size_t)b * H + head) * hd;
         dst[i] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
@@ -123,11 +124,11 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
     if (p < 0 || p >= L) return;
     const int kh = head - H;
     const size_t hb = (size_t)b * Hkv + kh;
-    const uint16_t* src = k + hb * hd;
+    const uint16_t* src = k + (size_t)b * ldk + (size_t)kh * hd;
     const float x1 = bf(src[i]), x2 = bf(src[i + half]);
     kt[(hb * hd + i) * L + p] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
     kt[(hb * hd + i + half) * L + p] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s))));
-    const uint16_t* vs = v + hb * hd;
+    const uint16_t* vs = v + (size_t)b * ldv + (size_t)kh * hd;
     vc[(hb * L + p) * hd + i] = bf(vs[i]);
     vc[(hb * L + p) * hd + i + half] = bf(vs[i + half]);
 }
@@ -221,13 +222,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 }
 
 // out = bf16(bf16(silu(g)) * u), silu(x) = x / (1 + exp(-x)) in fp32 (F.silu then the product of
-// MLP.forward).
+// MLP.forward), over rows of n elements: row r of g / u starts ld elements after row r - 1 (the
+// two halves of one fused projection), out is [rows, n].
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
-                                uint16_t* __restrict__ out, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+                                uint16_t* __restrict__ out, int rows, int n, int64_t ld) {
+    const int64_t total = (int64_t)rows * n;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / n, i = r * ld + (e - r * n);
         const float x = bf(g[i]);
         const float sv = bf(to_bf(__fdiv_rn(x, __fadd_rn(1.f, expf(-x)))));
-        out[i] = to_bf(__fmul_rn(sv, bf(u[i])));
+        out[e] = to_bf(__fmul_rn(sv, bf(u[i])));
     }
 }
 
@@ -252,13 +256,17 @@ int tfp8_llm_add_rmsnorm(const void* x, const void* r, void* h, void* y, const v
     return launched();
 }
 
+// Row strides ldq >= H hd, ldk and ldv >= Hkv hd (elements).
 int tfp8_llm_rope_cache(const void* q, const void* k, const void* v, const float* cs, const float* sn, float* qf,
-                        float* kt, float* vc, const int64_t* pos, int B, int H, int Hkv, int hd, int L, void* stream) {
+                        float* kt, float* vc, const int64_t* pos, int B, int H, int Hkv, int hd, int L, int ldq,
+                        int ldk, int ldv, void* stream) {
     if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 512 || L <= 0) return -1;
+    if (ldq < H * hd || ldk < Hkv * hd || ldv < Hkv * hd) return -1;
     if (!q || !k || !v || !cs || !sn || !qf || !kt || !vc || !pos) return -1;
     if (B == 0) return 0;
     rope_cache_kernel<<<dim3(H + Hkv, B), hd / 2, 0, (hipStream_t)stream>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, qf, kt, vc, pos, H, Hkv, hd, L);
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, qf, kt, vc, pos, H, Hkv, hd, L, ldq, ldk,
+        ldv);
     return launched();
 }
 
@@ -277,12 +285,13 @@ int tfp8_llm_attention(const float* qf, const float* kt, const float* vc, const 
     return launched();
 }
 
-int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int64_t n, void* stream) {
-    if (n < 0 || !g || !u || !out) return -1;
-    if (n == 0) return 0;
-    const int64_t blocks = (n + 255) / 256;
+// rows x n elements, input row stride ld >= n.
+int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int rows, int n, int64_t ld, void* stream) {
+    if (rows < 0 || n < 0 || ld < n || !g || !u || !out) return -1;
+    if (rows == 0 || n == 0) return 0;
+    const int64_t blocks = ((int64_t)rows * n + 255) / 256;
     silu_mul_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, (hipStream_t)stream>>>(
-        (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, n);
+        (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, rows, n, ld);
     return launched();
 }
 

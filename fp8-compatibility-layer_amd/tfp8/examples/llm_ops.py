@@ -22,9 +22,9 @@ def library():
         lib = ctypes.CDLL(_PATH)
         p, i, f, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64
         lib.tfp8_llm_add_rmsnorm.argtypes = [p, p, p, p, p, i, i, f, p]
-        lib.tfp8_llm_rope_cache.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, p]
+        lib.tfp8_llm_rope_cache.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p]
         lib.tfp8_llm_attention.argtypes = [p, p, p, p, p, i, p, i, i, i, i, i, f, p]
-        lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i64, p]
+        lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i, i, i64, p]
         for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul):
             fn.restype = ctypes.c_int
         _LIB = lib
@@ -43,6 +43,17 @@ def _check(rc, what):
 def _bf16(t, what):
     if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
         raise ValueError(f"{what}: contiguous bfloat16 CUDA tensor expected, got {t.dtype} {t.device}")
+
+
+def _rows(t, n, what):
+    """(rows, row stride) of a bf16 CUDA tensor [..., n] whose rows are contiguous (a contiguous tensor
+    or a column slice of one, such as a part of a fused projection's output)."""
+    if t.dtype != torch.bfloat16 or not t.is_cuda or t.shape[-1] != n:
+        raise ValueError(f"{what}: bfloat16 CUDA tensor [..., {n}] expected, got {t.dtype} {tuple(t.shape)}")
+    r = t.reshape(-1, n)
+    if r.data_ptr() != t.data_ptr() or (n > 1 and r.stride(1) != 1) or (r.shape[0] > 1 and r.stride(0) < n):
+        raise ValueError(f"{what}: rows of {n} contiguous elements expected")
+    return r.shape[0], (r.stride(0) if r.shape[0] > 1 else n)
 
 
 def add_rmsnorm(x, r, weight, eps):
@@ -67,14 +78,14 @@ def add_rmsnorm(x, r, weight, eps):
 
 
 def rope_cache(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
-    """Rotary embedding of one position's q, k (bf16 [B, 1, heads * hd]) with cos/sin (fp32 [hd / 2]),
-    k and v written (widened to fp32) into the caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at
-    position pos (int64 [1] on the device); returns the rotated q widened to fp32 [B, n_heads, hd]."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v")):
-        _bf16(t, n)
+    """Rotary embedding of one position's q, k (bf16 [B, 1, heads * hd], rows contiguous: column slices
+    of one fused projection are taken as they lie) with cos/sin (fp32 [hd / 2]), k and v written
+    (widened to fp32) into the caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at position pos
+    (int64 [1] on the device); returns the rotated q widened to fp32 [B, n_heads, hd]."""
     B, hd, L = q.shape[0], kt.shape[2], kt.shape[3]
-    if q.numel() != B * n_heads * hd or k.numel() != B * n_kv * hd or v.numel() != k.numel():
-        raise ValueError("q/k/v sizes do not match the heads")
+    (bq, ldq), (bk, ldk), (bv, ldv) = _rows(q, n_heads * hd, "q"), _rows(k, n_kv * hd, "k"), _rows(v, n_kv * hd, "v")
+    if not bq == bk == bv == B:
+        raise ValueError("q/k/v rows do not match the batch")
     if tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
         raise ValueError(f"cache shapes {tuple(kt.shape)} / {tuple(vc.shape)}")
     for t, n in ((kt, "kt"), (vc, "vc"), (cos, "cos"), (sin, "sin")):
@@ -85,7 +96,7 @@ def rope_cache(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
     qf = torch.empty(B, n_heads, hd, dtype=torch.float32, device=q.device)
     _check(library().tfp8_llm_rope_cache(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                          qf.data_ptr(), kt.data_ptr(), vc.data_ptr(), pos.data_ptr(), B, n_heads, n_kv,
-                                         hd, L, _stream(q)), "rope_cache")
+                                         hd, L, ldq, ldk, ldv, _stream(q)), "rope_cache")
     return qf
 
 
@@ -107,11 +118,12 @@ def attention(qf, kt, vc, pos, n_heads, n_kv):
 
 
 def silu_mul(g, u):
-    """bf16(bf16(silu(g)) * u), elementwise."""
-    _bf16(g, "g")
-    _bf16(u, "u")
-    if g.shape != u.shape:
-        raise ValueError(f"g {tuple(g.shape)} and u {tuple(u.shape)} differ")
-    out = torch.empty_like(g)
-    _check(library().tfp8_llm_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(), _stream(g)), "silu_mul")
+    """bf16(bf16(silu(g)) * u), elementwise over [..., n] (rows contiguous, with one row stride for
+    both: separate tensors or the two halves of one fused projection); returns a new [..., n]."""
+    n = g.shape[-1]
+    (rg, ldg), (ru, ldu) = _rows(g, n, "g"), _rows(u, n, "u")
+    if g.shape != u.shape or rg != ru or (rg > 1 and ldg != ldu):
+        raise ValueError(f"g {tuple(g.shape)} and u {tuple(u.shape)} differ in shape or row stride")
+    out = torch.empty(g.shape, dtype=g.dtype, device=g.device)
+    _check(library().tfp8_llm_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), rg, n, ldg, _stream(g)), "silu_mul")
     return out

@@ -249,6 +249,14 @@ def test_llm_ops_match_pytorch_forms():
         kt2.index_copy_(3, pos, k_ref.permute(0, 2, 3, 1).float())
         vc2.index_copy_(2, pos, v.view(B, 1, Hkv, hd).transpose(1, 2).float())
         assert torch.equal(kt, kt2) and torch.equal(vc, vc2)
+        # the same from column slices of one fused projection output, and SiLU * up from its halves
+        fusedo = torch.cat([q, k, v], -1)
+        kt3, vc3 = kt.clone(), vc.clone()
+        qf3 = ops.rope_cache(fusedo[..., :H * hd], fusedo[..., H * hd:(H + Hkv) * hd], fusedo[..., (H + Hkv) * hd:],
+                             cos.reshape(-1), sin.reshape(-1), kt3, vc3, pos, H, Hkv)
+        assert torch.equal(qf3, qf) and torch.equal(kt3, kt) and torch.equal(vc3, vc)
+        gu = torch.cat([gg, uu], -1)
+        assert torch.equal(ops.silu_mul(gu[..., :4 * d], gu[..., 4 * d:]), ops.silu_mul(gg, uu))
 
         o = ops.attention(qf, kt, vc, pos, H, Hkv)
         rep = H // Hkv

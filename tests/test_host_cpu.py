@@ -343,11 +343,12 @@ def test_example_ops_library_loads_and_validates_without_gpu():
     assert lib.tfp8_llm_add_rmsnorm(a, None, None, a, a, 1, 12, 1e-5, None) == -1        # d % 8
     assert lib.tfp8_llm_add_rmsnorm(a + 2, None, None, a, a, 1, 16, 1e-5, None) == -1    # alignment
     assert lib.tfp8_llm_add_rmsnorm(a, None, None, a, a, 0, 16, 1e-5, None) == 0         # no rows
-    assert lib.tfp8_llm_rope_cache(a, a, a, a, a, a, a, a, a, 1, 6, 4, 128, 64, None) == -1   # H % Hkv
+    assert lib.tfp8_llm_rope_cache(a, a, a, a, a, a, a, a, a, 1, 6, 4, 128, 64, 768, 512, 512, None) == -1   # H % Hkv
+    assert lib.tfp8_llm_rope_cache(a, a, a, a, a, a, a, a, a, 1, 8, 4, 128, 64, 768, 512, 512, None) == -1   # ldq < H hd
     assert lib.tfp8_llm_attention(a, a, a, a, a, 2, a, 1, 4, 4, 96, 64, 1.0, None) == -1     # head dim
     assert lib.tfp8_llm_attention(a, a, a, a, a, 1, a, 1, 4, 4, 128, 65, 1.0, None) == -1    # S * 64 < L
-    assert lib.tfp8_llm_silu_mul(a, a, a, -1, None) == -1
-    assert lib.tfp8_llm_silu_mul(a, a, a, 0, None) == 0
+    assert lib.tfp8_llm_silu_mul(a, a, a, 2, 16, 8, None) == -1        # row stride below the row
+    assert lib.tfp8_llm_silu_mul(a, a, a, 0, 16, 16, None) == 0
 
 
 def test_available_false_and_require_raises_without_gpu():
