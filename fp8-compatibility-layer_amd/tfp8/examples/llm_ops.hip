@@ -235,6 +235,51 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* 
     }
 }
 
+// Tied output head of the decode step: y[b, v] = sum_k float(x[b, k]) * float(w[v, k]) with fp32
+// accumulation, x the normed hidden state (bf16 [NB, K]) and w the bf16 embedding [V, K] -- the
+// products of Llama._head's F.linear(x.float(), embedding.float()), read from the bf16 embedding
+// itself instead of an fp32 copy of it.  Block of 4 waves, 4 embedding rows per wave; x widened
+// into LDS; lane l takes k = 512 it + 8 l .. + 7 (K % 512 == 0).
+template <int NB>
+__global__ __launch_bounds__(256) void head_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                   float* __restrict__ y, int V, int K) {
+    extern __shared__ float xs[];                  // NB * K
+    for (int i = threadIdx.x; i < NB * K; i += 256) xs[i] = bf(x[i]);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + wave) * 4;
+    if (r0 >= V) return;
+    float acc[4][NB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
+    for (int k = lane * 8; k < K; k += 512) {
+        uint4 wv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            wv[r] = r0 + r < V ? *(const uint4*)(w + (size_t)(r0 + r) * K + k) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float4 xa = *(const float4*)(xs + b * K + k), xb = *(const float4*)(xs + b * K + k + 4);
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint16_t* wr = (const uint16_t*)&wv[r];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[r][b] = fmaf(xv[j], bf(wr[j]), acc[r][b]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float t = wave_sum(acc[r][b]);
+            if (lane == 0 && r0 + r < V) y[(size_t)b * V + r0 + r] = t;
+        }
+}
+
 int launched() { return (int)hipGetLastError(); }
 
 }  // namespace
@@ -292,6 +337,29 @@ int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int rows, int n, 
     const int64_t blocks = ((int64_t)rows * n + 255) / 256;
     silu_mul_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, rows, n, ld);
+    return launched();
+}
+
+
+// rows <= 8, K % 512 == 0, rows * K <= 16384 (x widened into 64 KB of LDS).
+int tfp8_llm_head(const void* x, const void* w, float* y, int rows, int V, int K, void* stream) {
+    if (rows < 0 || rows > 8 || V < 0 || K <= 0 || K % 512 || (int64_t)rows * K > 16384 || !x || !w || !y) return -1;
+    if (((uintptr_t)x | (uintptr_t)w) % 16) return -1;
+    if (rows == 0 || V == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    const unsigned grid = (unsigned)((V + 15) / 16);
+    const size_t lds = (size_t)rows * K * sizeof(float);
+    const uint16_t *xp = (const uint16_t*)x, *wp = (const uint16_t*)w;
+    switch (rows) {
+        case 1: head_kernel<1><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 2: head_kernel<2><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 3: head_kernel<3><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 4: head_kernel<4><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 5: head_kernel<5><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 6: head_kernel<6><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        case 7: head_kernel<7><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+        default: head_kernel<8><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
+    }
     return launched();
 }
 

@@ -25,7 +25,9 @@ def library():
         lib.tfp8_llm_rope_cache.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, p]
         lib.tfp8_llm_attention.argtypes = [p, p, p, p, p, i, p, i, i, i, i, i, f, p]
         lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i, i, i64, p]
-        for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul):
+        lib.tfp8_llm_head.argtypes = [p, p, p, i, i, i, p]
+        for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul,
+                   lib.tfp8_llm_head):
             fn.restype = ctypes.c_int
         _LIB = lib
     return _LIB
@@ -127,3 +129,18 @@ def silu_mul(g, u):
     out = torch.empty(g.shape, dtype=g.dtype, device=g.device)
     _check(library().tfp8_llm_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), rg, n, ldg, _stream(g)), "silu_mul")
     return out
+
+
+def head(x, weight):
+    """Logits fp32 [..., V] = x (bf16 [..., K], at most 8 rows) times weight (bf16 [V, K])
+    transposed, with fp32 products and sums: F.linear(x.float(), weight.float()) without widening
+    the weight in memory."""
+    _bf16(x, "x")
+    _bf16(weight, "weight")
+    V, K = weight.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"x {tuple(x.shape)} does not match the weight {tuple(weight.shape)}")
+    y = torch.empty(*x.shape[:-1], V, dtype=torch.float32, device=x.device)
+    _check(library().tfp8_llm_head(x.data_ptr(), weight.data_ptr(), y.data_ptr(), x.numel() // K, V, K, _stream(x)),
+           "head")
+    return y

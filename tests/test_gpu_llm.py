@@ -258,6 +258,14 @@ def test_llm_ops_match_pytorch_forms():
         gu = torch.cat([gg, uu], -1)
         assert torch.equal(ops.silu_mul(gu[..., :4 * d], gu[..., 4 * d:]), ops.silu_mul(gg, uu))
 
+        # tied head from the bf16 embedding: F.linear of the widened operands, fp32 sums reordered
+        emb = (0.02 * torch.randn(1000, d, device="cuda", generator=g)).bfloat16()
+        for rows in (1, 3, 8):
+            xh = torch.randn(rows, 1, d, device="cuda", generator=g).bfloat16()
+            got, want = ops.head(xh, emb), torch.nn.functional.linear(xh.float(), emb.float())
+            bound = 1e-5 * torch.nn.functional.linear(xh.float().abs(), emb.float().abs())
+            assert got.shape == want.shape and ((got - want).abs() <= bound).all(), rows
+
         o = ops.attention(qf, kt, vc, pos, H, Hkv)
         rep = H // Hkv
         scores = torch.matmul(qf.view(B, H, 1, hd), kt.repeat_interleave(rep, 1)) / (hd ** 0.5)

@@ -332,11 +332,11 @@ def test_abi_argument_validation_without_gpu():
 
 
 def test_example_ops_library_loads_and_validates_without_gpu():
-    """libtfp8_llm.so (the example model's fused decode ops) exports its four entry points and
+    """libtfp8_llm.so (the example model's fused decode ops) exports its five entry points and
     refuses arguments its kernels do not take before launching anything."""
     from tfp8.examples import llm_ops
     lib = llm_ops.library()
-    for n in ("tfp8_llm_add_rmsnorm", "tfp8_llm_rope_cache", "tfp8_llm_attention", "tfp8_llm_silu_mul"):
+    for n in ("tfp8_llm_add_rmsnorm", "tfp8_llm_rope_cache", "tfp8_llm_attention", "tfp8_llm_silu_mul", "tfp8_llm_head"):
         assert hasattr(lib, n), n
     buf = ctypes.create_string_buffer(4096)
     a = (ctypes.addressof(buf) + 255) & ~255
@@ -349,6 +349,8 @@ def test_example_ops_library_loads_and_validates_without_gpu():
     assert lib.tfp8_llm_attention(a, a, a, a, a, 1, a, 1, 4, 4, 128, 65, 1.0, None) == -1    # S * 64 < L
     assert lib.tfp8_llm_silu_mul(a, a, a, 2, 16, 8, None) == -1        # row stride below the row
     assert lib.tfp8_llm_silu_mul(a, a, a, 0, 16, 16, None) == 0
+    assert lib.tfp8_llm_head(a, a, a, 9, 100, 512, None) == -1           # more than 8 rows
+    assert lib.tfp8_llm_head(a, a, a, 1, 100, 520, None) == -1           # K % 512
 
 
 def test_available_false_and_require_raises_without_gpu():
