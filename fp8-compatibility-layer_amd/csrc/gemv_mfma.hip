@@ -284,8 +284,13 @@ int run_gemv_mfma(const void* x, int x_dtype, const float* xs, int M, int K, con
     if (sm == SM_F32 && G % 64) return NOT_TAKEN;
     const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
     // Config: two 16-row weight tiles per block, K split over 4 waves, 4 chunks in flight per wave
-    // (sweep on MI355X at C2 M=4/8; knobs TFP8_GM_NT / _W / _D).
-    const int NT = tune(TUNE_GM_NT), W = tune(TUNE_GM_W), D = tune(TUNE_GM_D);
+    // (sweep on MI355X at C2 M=4/8) while that gives a block per CU; below N = 8192 one tile per
+    // block (twice the blocks), 8 waves, 8 chunks in flight (M=5/8/16, N=2048, K=5632, an LLM
+    // down projection: 12.1/12.6/14.3 -> 8.2/9.0/10.8 us).  Knobs TFP8_GM_NT / _W / _D force them.
+    const bool few = N < 16 * 2 * 256;
+    const int NT = tune(TUNE_GM_NT) > 0 ? tune(TUNE_GM_NT) : few ? 1 : 2;
+    const int W = tune(TUNE_GM_W) > 0 ? tune(TUNE_GM_W) : few ? 8 : 4;
+    const int D = tune(TUNE_GM_D) > 0 ? tune(TUNE_GM_D) : few ? 8 : 4;
     const int sbytes = sm == SM_CHANNEL ? 0 : (16 * NT * ng * (sm == SM_F32 ? 4 : 1) + 15) / 16 * 16;
     // Transposed weight loads (C2 M=4: 18.1 -> 15.0 us, M=8: 19.4 -> 15.4 us; identical results)
     // need whole 256-code groups in every wave's K range; knob TFP8_GM_TL=0 keeps the direct layout.

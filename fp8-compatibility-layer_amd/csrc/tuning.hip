@@ -27,9 +27,9 @@ constexpr KnobDef KNOBS[TUNE_COUNT] = {
     {"TFP8_GEMV_WPC", 0},            // streaming GEMV waves per CU (0: the configuration's own)
     {"TFP8_GEMV_MFMA_MIN", 4},       // smallest M for the matrix-core decode kernel
     {"TFP8_GEMV_MFMA_MAX_M", 16},    // largest M for the matrix-core decode kernel on the GEMM entry
-    {"TFP8_GM_NT", 2},               // decode kernel: 16-row weight tiles per block
-    {"TFP8_GM_W", 4},                // decode kernel: waves per block (K split)
-    {"TFP8_GM_D", 4},                // decode kernel: chunks in flight per wave
+    {"TFP8_GM_NT", 0},               // decode kernel: 16-row weight tiles per block (0: by N)
+    {"TFP8_GM_W", 0},                // decode kernel: waves per block, the K split (0: by N)
+    {"TFP8_GM_D", 0},                // decode kernel: chunks in flight per wave (0: by N)
     {"TFP8_GM_TL", 1},               // decode kernel: transposed (4 rows x 256 B) weight loads
     {"TFP8_GEMM_TILE", 0},           // LDS-tiled GEMM configuration index (0: by M)
     {"TFP8_GEMM_SPLITK", 0},         // split-K of the tiled and direct GEMMs (0: by shape)

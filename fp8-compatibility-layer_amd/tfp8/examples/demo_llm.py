@@ -470,10 +470,35 @@ def run(size="c5", prompt_len=512, n_decode=128, batches=(1, 8)):
     return dict(cos=cos, rel=rel, top1=top1)
 
 
+@torch.no_grad()
+def graph_decode(size="c5", B=1, prompt_len=512, n_decode=128):
+    """Only the FP8 model's HIP-graph decode (for kernel profiles): convert, capture, prefill, then
+    n_decode replayed steps; returns ms per token."""
+    from tfp8 import FP8Config, prepare_model
+    model = build(size)
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn"))
+    ids = torch.randint(0, model.c["vocab"], (B, prompt_len), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+    dec = GraphDecoder(model, B, prompt_len + n_decode).capture()
+    dec.prefill(ids)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(n_decode):
+        dec.step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / n_decode
+    print(f"{size} B={B}: graph decode {ms:.3f} ms per token over {n_decode} steps after a {prompt_len}-token prompt")
+    return ms
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--size", default="c5", choices=list(SIZES))
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--decode", type=int, default=128)
+    ap.add_argument("--graph-decode", type=int, default=None, metavar="B",
+                    help="only time the FP8 model's graph decode at batch B (for kernel profiles)")
     a = ap.parse_args()
-    run(a.size, a.prompt_len, a.decode)
+    if a.graph_decode:
+        graph_decode(a.size, a.graph_decode, a.prompt_len, a.decode)
+    else:
+        run(a.size, a.prompt_len, a.decode)
