@@ -43,7 +43,7 @@ constexpr KnobDef KNOBS[TUNE_COUNT] = {
     {"TFP8_GEMM_V1", 0},             // skip the weight-streaming GEMM (LDS-tiled kernel instead)
     {"TFP8_GEMV_PAIR", 1},           // row-pair GEMV where it applies (0 off, 1 auto, 4/8 waves per block at M = 1)
     {"TFP8_GEMV_PAIR_MAX_M", 4},     // largest M (1..4) for the row-pair GEMV
-    {"TFP8_GEMV_QUAD", 1},           // 4x4x4-MFMA GEMV: 0 off, 1 one scale per row, 2 K-group scales too
+    {"TFP8_GEMV_QUAD", 1},           // 4x4x4-MFMA GEMV: 0 off, 1 default (K groups up to 4 rows), 2 K groups up to 8
     {"TFP8_GEMV_QUAD_MIN_M", 3},     // smallest M for the 4x4x4-MFMA GEMV
 };
 
