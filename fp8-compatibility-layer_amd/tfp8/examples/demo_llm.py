@@ -7,10 +7,9 @@ The model is built here (random N(0, 0.02) init, tied embedding / output head), 
 prepare_model(profile="llm_safe"), and measured the way the reference demo measures it: logits
 agreement with the bf16 model (cosine, relative L2, top-1), prefill and per-token decode latency,
 and the FP8Linear path counters.  Layout choices for the GPU:
-  * the KV cache is preallocated in fp32 and written in place, keys as [B, heads, head_dim, max_len]
-    and values as [B, heads, max_len, head_dim], so both attention products read the cache as it
-    lies (no per-step widening or transposed copy of the whole cache); the cached values are the
-    bf16 projections widened exactly, the same numbers a bf16 cache read back in fp32 holds;
+  * the KV cache is preallocated in the model's dtype and written in place, keys as [B, heads,
+    head_dim, max_len] and values as [B, heads, max_len, head_dim], so the fused attention reads
+    both as they lie (no transposed copy of the keys); the PyTorch forms widen what they read;
   * attention runs in fp32 (scores, causal mask, softmax, values);
   * the tied output head keeps one fp32 copy of the embedding (the reference re-widens the
     embedding to fp32 on every call, demo_llm.py:127);
@@ -81,7 +80,7 @@ class Attention(nn.Module):
         vc[:, :, start:start + T] = v.transpose(1, 2)
         L = start + T
         rep = self.nh // self.nkv
-        keys_t, vals = kt[:, :, :, :L], vc[:, :, :L]                         # [B, Hkv, hd, L], [B, Hkv, L, hd]
+        keys_t, vals = kt[:, :, :, :L].float(), vc[:, :, :L].float()         # [B, Hkv, hd, L], [B, Hkv, L, hd]
         if rep > 1:
             keys_t, vals = keys_t.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
         qf = q.transpose(1, 2).float().contiguous()                          # [B, H, T, hd]
@@ -102,10 +101,10 @@ class Attention(nn.Module):
         k = _rotary(self.k_proj(x).view(B, T, self.nkv, self.hd), cos, sin)
         v = self.v_proj(x).view(B, T, self.nkv, self.hd)
         kt, vc = cache
-        kt.index_copy_(3, pos, k.permute(0, 2, 3, 1).float())
-        vc.index_copy_(2, pos, v.transpose(1, 2).float())
+        kt.index_copy_(3, pos, k.permute(0, 2, 3, 1))
+        vc.index_copy_(2, pos, v.transpose(1, 2))
         rep = self.nh // self.nkv
-        keys_t, vals = kt, vc
+        keys_t, vals = kt.float(), vc.float()
         if rep > 1:
             keys_t, vals = keys_t.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
         qf = q.transpose(1, 2).float().contiguous()                          # [B, H, 1, hd]
@@ -158,12 +157,13 @@ class Llama(nn.Module):
         self._head32 = None
 
     def new_cache(self, B, max_len, zero=False):
-        """Per layer (keys [B, n_kv, head_dim, max_len], values [B, n_kv, max_len, head_dim]), fp32."""
+        """Per layer (keys [B, n_kv, head_dim, max_len], values [B, n_kv, max_len, head_dim]) in the
+        model's dtype."""
         c, p = self.c, self.embed.weight
         hd = c["dim"] // c["n_heads"]
         new = torch.zeros if zero else torch.empty
-        return [(new(B, c["n_kv"], hd, max_len, dtype=torch.float32, device=p.device),
-                 new(B, c["n_kv"], max_len, hd, dtype=torch.float32, device=p.device)) for _ in self.layers]
+        return [(new(B, c["n_kv"], hd, max_len, dtype=p.dtype, device=p.device),
+                 new(B, c["n_kv"], max_len, hd, dtype=p.dtype, device=p.device)) for _ in self.layers]
 
     def _rope(self, start, T, device):
         hd = self.c["dim"] // self.c["n_heads"]

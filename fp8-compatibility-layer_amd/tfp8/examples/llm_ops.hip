@@ -101,14 +101,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
 // Rotary embedding of one position and the KV-cache write (demo_llm._rotary and the index_copy_ of
 // Attention.forward_static): x = [x1, x2] -> bf16([x1 c - x2 s, x2 c + x1 s]).  Block (head, b),
 // hd / 2 threads: heads below H are query heads (out: qf [B, H, hd] fp32, the rotated bf16 values
-// widened); the next Hkv are key heads, written widened into kt [B, Hkv, hd, L] at column *pos,
-// with the value head into vc [B, Hkv, L, hd] at row *pos.  Row b of q / k / v starts ldq / ldk /
+// widened); the next Hkv are key heads, written into the bf16 cache kt [B, Hkv, hd, L] at column
+// *pos, with the value head into vc [B, Hkv, L, hd] at row *pos.  Row b of q / k / v starts ldq / ldk /
 // ldv elements after row b - 1 (slices of one fused projection).  A position outside the cache
 // writes nothing (the host checks it; this only keeps a bad position from writing out of bounds).
 __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                   const uint16_t* __restrict__ v, const float* __restrict__ cs,
-                                  const float* __restrict__ sn, float* __restrict__ qf, float* __restrict__ kt,
-                                  float* __restrict__ vc, const int64_t* __restrict__ pos, int H, int Hkv, int hd,
+                                  const float* __restrict__ sn, float* __restrict__ qf, uint16_t* __restrict__ kt,
+                                  uint16_t* __restrict__ vc, const int64_t* __restrict__ pos, int H, int Hkv, int hd,
                                   int L, int ldq, int ldk, int ldv) {
     const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = hd / 2;
     const float c = cs[i], s = sn[i];
@@ -126,23 +126,24 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
     const size_t hb = (size_t)b * Hkv + kh;
     const uint16_t* src = k + (size_t)b * ldk + (size_t)kh * hd;
     const float x1 = bf(src[i]), x2 = bf(src[i + half]);
-    kt[(hb * hd + i) * L + p] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
-    kt[(hb * hd + i + half) * L + p] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s))));
+    kt[(hb * hd + i) * L + p] = to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
+    kt[(hb * hd + i + half) * L + p] = to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s)));
     const uint16_t* vs = v + (size_t)b * ldv + (size_t)kh * hd;
-    vc[(hb * L + p) * hd + i] = bf(vs[i]);
-    vc[(hb * L + p) * hd + i + half] = bf(vs[i + half]);
+    vc[(hb * L + p) * hd + i] = vs[i];
+    vc[(hb * L + p) * hd + i + half] = vs[i + half];
 }
 
 // Decode attention over cache positions 0..*pos, split over gridDim.y chunks of at most 64
-// positions.  Block (b * H + h, j), 4 waves: lane l takes position t0 + l, wave w the dot product
+// positions of the bf16 caches (widened as read).  Block (b * H + h, j), 4 waves: lane l takes
+// position t0 + l, wave w the dot product
 // over head dimensions [w HD/4, (w+1) HD/4) (every load of a lane in flight at once), summed over
 // the waves in LDS: s_t = (q . k_t) / sdiv.  Then m = max s_t, l = sum exp(s_t - m) and
 // o[i] = sum exp(s_t - m) v_t[i], stored as part[(bh * S + j) * (HD + 2) + {0: m, 1: l, 2 + i: o[i]}]
 // (an empty chunk stores m = -inf, l = 0, o = 0).  Query head h reads key/value head h / (H / Hkv)
 // (repeat_interleave over heads).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict__ qf, const float* __restrict__ kt,
-                                                        const float* __restrict__ vc, const int64_t* __restrict__ pos,
+__global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict__ qf, const uint16_t* __restrict__ kt,
+                                                        const uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
                                                         float* __restrict__ part, int H, int Hkv, int L, float sdiv) {
     constexpr int Q = HD / 4, G = 256 / HD;
     __shared__ float qs[HD], dots[4][64], e[64], oacc[256];
@@ -154,10 +155,10 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
     if (tid < HD) qs[tid] = qf[(size_t)bh * HD + tid];
     __syncthreads();
     if (lane < cnt) {
-        const float* kp = kt + (hb * HD + w * Q) * L + t0 + lane;
+        const uint16_t* kp = kt + (hb * HD + w * Q) * L + t0 + lane;
         float kv[Q];
 #pragma unroll
-        for (int i = 0; i < Q; ++i) kv[i] = kp[(size_t)i * L];
+        for (int i = 0; i < Q; ++i) kv[i] = bf(kp[(size_t)i * L]);
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < Q; ++i) dot = fmaf(qs[w * Q + i], kv[i], dot);
@@ -177,10 +178,10 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
     __syncthreads();
     // o: G groups of HD threads; group g sums positions g, g + G, ... (loads independent of the sums)
     const int g = tid / HD, i = tid - g * HD;
-    const float* vp = vc + (hb * L + t0) * HD + i;
+    const uint16_t* vp = vc + (hb * L + t0) * HD + i;
     float acc = 0.f;
 #pragma unroll 8
-    for (int t = g; t < cnt; t += G) acc = fmaf(e[t], vp[(size_t)t * HD], acc);
+    for (int t = g; t < cnt; t += G) acc = fmaf(e[t], bf(vp[(size_t)t * HD]), acc);
     oacc[tid] = acc;
     __syncthreads();
     float* out = part + ((size_t)bh * S + j) * (HD + 2);
@@ -303,27 +304,29 @@ int tfp8_llm_add_rmsnorm(const void* x, const void* r, void* h, void* y, const v
 
 // Row strides ldq >= H hd, ldk and ldv >= Hkv hd (elements).
 int tfp8_llm_rope_cache(const void* q, const void* k, const void* v, const float* cs, const float* sn, float* qf,
-                        float* kt, float* vc, const int64_t* pos, int B, int H, int Hkv, int hd, int L, int ldq,
+                        void* kt, void* vc, const int64_t* pos, int B, int H, int Hkv, int hd, int L, int ldq,
                         int ldk, int ldv, void* stream) {
     if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 512 || L <= 0) return -1;
     if (ldq < H * hd || ldk < Hkv * hd || ldv < Hkv * hd) return -1;
     if (!q || !k || !v || !cs || !sn || !qf || !kt || !vc || !pos) return -1;
     if (B == 0) return 0;
     rope_cache_kernel<<<dim3(H + Hkv, B), hd / 2, 0, (hipStream_t)stream>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, qf, kt, vc, pos, H, Hkv, hd, L, ldq, ldk,
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, qf, (uint16_t*)kt, (uint16_t*)vc, pos, H,
+        Hkv, hd, L, ldq, ldk,
         ldv);
     return launched();
 }
 
 // Chunks S with S * 64 >= L and S <= 256; head dimension 64 or 128; part holds B * H * S * (hd + 2) floats.
-int tfp8_llm_attention(const float* qf, const float* kt, const float* vc, const int64_t* pos, float* part, int S,
+int tfp8_llm_attention(const float* qf, const void* kt, const void* vc, const int64_t* pos, float* part, int S,
                        void* out, int B, int H, int Hkv, int hd, int L, float sdiv, void* stream) {
     if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || L <= 0) return -1;
     if (S <= 0 || (int64_t)S * 64 < L || S > 256 || !qf || !kt || !vc || !pos || !part || !out) return -1;
     if (B == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
-    if (hd == 128) attn_part_kernel<128><<<dim3(B * H, S), 256, 0, s>>>(qf, kt, vc, pos, part, H, Hkv, L, sdiv);
-    else attn_part_kernel<64><<<dim3(B * H, S), 256, 0, s>>>(qf, kt, vc, pos, part, H, Hkv, L, sdiv);
+    const uint16_t *kp = (const uint16_t*)kt, *vp = (const uint16_t*)vc;
+    if (hd == 128) attn_part_kernel<128><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv);
+    else attn_part_kernel<64><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv);
     int rc = launched();
     if (rc) return rc;
     attn_combine_kernel<<<B * H, 256, 0, s>>>(part, (uint16_t*)out, hd, S);

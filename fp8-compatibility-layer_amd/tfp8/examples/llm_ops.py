@@ -82,15 +82,17 @@ def add_rmsnorm(x, r, weight, eps):
 def rope_cache(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
     """Rotary embedding of one position's q, k (bf16 [B, 1, heads * hd], rows contiguous: column slices
     of one fused projection are taken as they lie) with cos/sin (fp32 [hd / 2]), k and v written
-    (widened to fp32) into the caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at position pos
-    (int64 [1] on the device); returns the rotated q widened to fp32 [B, n_heads, hd]."""
+    into the bf16 caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at position pos (int64 [1] on the
+    device); returns the rotated q widened to fp32 [B, n_heads, hd]."""
     B, hd, L = q.shape[0], kt.shape[2], kt.shape[3]
     (bq, ldq), (bk, ldk), (bv, ldv) = _rows(q, n_heads * hd, "q"), _rows(k, n_kv * hd, "k"), _rows(v, n_kv * hd, "v")
     if not bq == bk == bv == B:
         raise ValueError("q/k/v rows do not match the batch")
     if tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
         raise ValueError(f"cache shapes {tuple(kt.shape)} / {tuple(vc.shape)}")
-    for t, n in ((kt, "kt"), (vc, "vc"), (cos, "cos"), (sin, "sin")):
+    _bf16(kt, "kt")
+    _bf16(vc, "vc")
+    for t, n in ((cos, "cos"), (sin, "sin")):
         if t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError(f"{n}: contiguous float32 expected")
     if cos.numel() != hd // 2 or sin.numel() != hd // 2 or pos.dtype != torch.int64 or pos.numel() != 1:
@@ -104,7 +106,9 @@ def rope_cache(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
 
 def attention(qf, kt, vc, pos, n_heads, n_kv):
     """softmax((q . k_t) / sqrt(hd), t <= pos) weighted sum of v_t for every (batch, head), over the
-    caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] (fp32); returns bf16 [B, 1, n_heads * hd]."""
+    caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] (bf16); returns bf16 [B, 1, n_heads * hd]."""
+    _bf16(kt, "kt")
+    _bf16(vc, "vc")
     B, hd, L = qf.shape[0], kt.shape[2], kt.shape[3]
     if tuple(qf.shape) != (B, n_heads, hd) or qf.dtype != torch.float32 or not qf.is_contiguous():
         raise ValueError(f"qf {tuple(qf.shape)} {qf.dtype}")

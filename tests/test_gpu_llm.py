@@ -232,8 +232,8 @@ def test_llm_ops_match_pytorch_forms():
         # PyTorch ops (Attention.forward_static with the same caches)
         p = 217
         pos = torch.tensor([p], dtype=torch.long, device="cuda")
-        kt = torch.randn(B, Hkv, hd, L, device="cuda", generator=g)
-        vc = torch.randn(B, Hkv, L, hd, device="cuda", generator=g)
+        kt = torch.randn(B, Hkv, hd, L, device="cuda", generator=g).bfloat16()
+        vc = torch.randn(B, Hkv, L, hd, device="cuda", generator=g).bfloat16()
         kt2, vc2 = kt.clone(), vc.clone()
         q = torch.randn(B, 1, H * hd, device="cuda", generator=g).bfloat16()
         k = torch.randn(B, 1, Hkv * hd, device="cuda", generator=g).bfloat16()
@@ -246,8 +246,8 @@ def test_llm_ops_match_pytorch_forms():
         q_ref = demo_llm._rotary(q.view(B, 1, H, hd), c4, s4)
         k_ref = demo_llm._rotary(k.view(B, 1, Hkv, hd), c4, s4)
         assert torch.equal(qf, q_ref.view(B, H, hd).float())
-        kt2.index_copy_(3, pos, k_ref.permute(0, 2, 3, 1).float())
-        vc2.index_copy_(2, pos, v.view(B, 1, Hkv, hd).transpose(1, 2).float())
+        kt2.index_copy_(3, pos, k_ref.permute(0, 2, 3, 1))
+        vc2.index_copy_(2, pos, v.view(B, 1, Hkv, hd).transpose(1, 2))
         assert torch.equal(kt, kt2) and torch.equal(vc, vc2)
         # the same from column slices of one fused projection output, and SiLU * up from its halves
         fusedo = torch.cat([q, k, v], -1)
@@ -268,9 +268,9 @@ def test_llm_ops_match_pytorch_forms():
 
         o = ops.attention(qf, kt, vc, pos, H, Hkv)
         rep = H // Hkv
-        scores = torch.matmul(qf.view(B, H, 1, hd), kt.repeat_interleave(rep, 1)) / (hd ** 0.5)
+        scores = torch.matmul(qf.view(B, H, 1, hd), kt.float().repeat_interleave(rep, 1)) / (hd ** 0.5)
         scores = scores.masked_fill(torch.arange(L, device="cuda") > pos, float("-inf"))
-        o_ref32 = torch.matmul(torch.softmax(scores, -1), vc.repeat_interleave(rep, 1))     # [B, H, 1, hd]
+        o_ref32 = torch.matmul(torch.softmax(scores, -1), vc.float().repeat_interleave(rep, 1))   # [B, H, 1, hd]
         o_ref32 = o_ref32.transpose(1, 2).reshape(B, 1, H * hd)
         err = (o.float() - o_ref32).abs()
         assert (err <= 2.0 ** -8 * o_ref32.abs() + 1e-5).all(), err.max().item()
@@ -279,9 +279,9 @@ def test_llm_ops_match_pytorch_forms():
         for p in (0, L - 1):
             pos.fill_(p)
             o = ops.attention(qf, kt, vc, pos, H, Hkv)
-            sc = torch.matmul(qf.view(B, H, 1, hd), kt.repeat_interleave(rep, 1)) / (hd ** 0.5)
+            sc = torch.matmul(qf.view(B, H, 1, hd), kt.float().repeat_interleave(rep, 1)) / (hd ** 0.5)
             sc = sc.masked_fill(torch.arange(L, device="cuda") > pos, float("-inf"))
-            ref = torch.matmul(torch.softmax(sc, -1), vc.repeat_interleave(rep, 1)).transpose(1, 2).reshape(B, 1, H * hd)
+            ref = torch.matmul(torch.softmax(sc, -1), vc.float().repeat_interleave(rep, 1)).transpose(1, 2).reshape(B, 1, H * hd)
             assert ((o.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-5).all(), p
 
 
