@@ -214,14 +214,19 @@ class Llama(nn.Module):
         """Per layer (qkv, gate_up): one FP8Linear over the rows of q/k/v_proj and one over those of
         gate/up_proj, for the decode step -- the codes and scales are the separate layers' rows, so
         every output is the same row product, in two GEMV launches instead of five.  None where the
-        layers are not FP8Linear of one layout.  Rebuilt when the layers or their weights change;
-        the first decode step builds them (GraphDecoder's warm-up steps, outside graph capture)."""
+        layers are not FP8Linear of one layout.  The separate layers' buffers become views of the
+        fused ones (one copy of the weights; writes into either are seen by both).  Rebuilt when a
+        layer or one of its buffers is replaced; the first decode step builds them (GraphDecoder's
+        warm-up steps, outside graph capture)."""
         srcs = [(l.self_attn.q_proj, l.self_attn.k_proj, l.self_attn.v_proj, l.mlp.gate_proj, l.mlp.up_proj)
                 for l in self.layers]
-        key = tuple((id(m), (m.qweight if "qweight" in m._buffers else m.weight).data_ptr()) for t in srcs for m in t)
-        if self.__dict__.get("_fused_key") != key:        # kept in __dict__: not registered as submodules
+
+        def key():
+            return tuple((id(m), *(b.data_ptr() for b in m._buffers.values() if b is not None), id(m._parameters.get("weight")))
+                         for t in srcs for m in t)
+        if self.__dict__.get("_fused_key") != key():      # kept in __dict__: not registered as submodules
             self.__dict__["_fused_proj"] = [(_concat_fp8(t[:3]), _concat_fp8(t[3:])) for t in srcs]
-            self.__dict__["_fused_key"] = key
+            self.__dict__["_fused_key"] = key()
         return self.__dict__["_fused_proj"]
 
     def _decode_fused(self, x, cos, sin, cache, pos):
@@ -269,7 +274,13 @@ def _concat_fp8(mods):
     with torch.no_grad():
         q = torch.cat([f.qweight for f in mods])
         s = torch.cat([f.weight_scale for f in mods])
-    return FP8Linear.from_fp8_checkpoint(q, s, None, f0.fmt, out_dtype=f0.out_dtype, nan_check=f0.nan_check)
+    fused = FP8Linear.from_fp8_checkpoint(q, s, None, f0.fmt, out_dtype=f0.out_dtype, nan_check=f0.nan_check)
+    n0 = 0
+    for f in mods:                      # the layers' buffers become row ranges of the fused ones
+        n1 = n0 + f.out_features
+        f.qweight, f.weight_scale = fused.qweight[n0:n1], fused.weight_scale[n0:n1]
+        n0 = n1
+    return fused
 
 
 def greedy(logits):

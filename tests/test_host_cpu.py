@@ -353,6 +353,37 @@ def test_example_ops_library_loads_and_validates_without_gpu():
     assert lib.tfp8_llm_head(a, a, a, 1, 100, 520, None) == -1           # K % 512
 
 
+def test_demo_fused_projections_share_the_layers_weights():
+    """The example model's decode step runs q/k/v and gate/up as one FP8Linear each: their codes and
+    scales are the layers' rows concatenated, the layers' buffers become views of them (one copy;
+    an in-place write to a layer reaches the fused one), and they are built once per set of buffers."""
+    from tfp8 import FP8Config, prepare_model
+    from tfp8.examples import demo_llm
+
+    torch.manual_seed(0)
+    model = demo_llm.Llama(dict(dim=1024, n_layers=2, n_heads=8, n_kv=8, ffn=1024, vocab=64))
+    prepare_model(model, "llm", FP8Config(nan_check=False))
+    ids = torch.randint(0, 64, (1, 5))
+    with torch.no_grad():
+        before = model(ids, model.new_cache(1, 5), 0)
+    fused = model._fused_projections()
+    assert len(fused) == 2 and model._fused_projections() is fused
+    at, mlp = model.layers[1].self_attn, model.layers[1].mlp
+    qkv, gate_up = fused[1]
+    assert qkv.out_features == 3 * 1024 and gate_up.out_features == 2 * 1024
+    assert at.k_proj.qweight.data_ptr() == qkv.qweight[1024:].data_ptr()
+    assert mlp.up_proj.weight_scale.data_ptr() == gate_up.weight_scale[1024:].data_ptr()
+    with torch.no_grad():
+        assert torch.equal(model(ids, model.new_cache(1, 5), 0), before)
+        y = torch.randn(2, 1024).bfloat16()
+        sep = torch.cat([at.q_proj(y), at.k_proj(y), at.v_proj(y)], -1)
+        assert torch.allclose(qkv(y).float(), sep.float(), rtol=1e-2, atol=1e-3)
+        at.v_proj.qweight[3, 7] ^= 1
+    assert qkv.qweight[2048 + 3, 7] == at.v_proj.qweight[3, 7]
+    at.q_proj.qweight = at.q_proj.qweight.clone()          # a replaced buffer rebuilds the fused layers
+    assert model._fused_projections() is not fused
+
+
 def test_available_false_and_require_raises_without_gpu():
     if torch.cuda.is_available():
         pytest.skip("GPU present")
