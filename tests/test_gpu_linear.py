@@ -465,6 +465,38 @@ def test_row_pair_gemv_shapes(wpb, tune):
         _run(1, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=wpb * 100 + i)
 
 
+def test_row_pair_gemv_partial_chunk_shapes(tune):
+    """The row-pair GEMV at K other than 2048/4096/8192 (3, 5, 6, 7 chunks of 1 KB up to 4 activation
+    rows, 11, 12 up to 2, 14 chunks on the streaming GEMV; the last chunk partial when K % 1024 != 0, its lanes past K reading
+    zeros, x staged with zeros past K, K groups past the row reading zero scales): per-channel and
+    K-group scales, f32 and UE8M0, both formats, f16/bf16 activations, N odd at M = 1; against the
+    oracle, and M = 1 against the streaming GEMV it replaces for these shapes."""
+    tune(TFP8_GEMV_QUAD=0)
+    for i, (M, N, K, G, fmt, sf, xdt, out, bias) in enumerate([
+            (1, 2048, 5632, None, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, False),   # 5.5 chunks
+            (2, 1000, 5632, 128, "e5m2", "ue8m0", torch.float16, torch.float32, True),
+            (4, 514, 3072, 64, "e4m3fn", "f32", torch.bfloat16, torch.float16, True),          # 3 chunks, L = 4
+            (3, 998, 6144, 256, "e5m2", "f32", torch.bfloat16, torch.float32, True),
+            (4, 260, 7040, 128, "e4m3fn", "ue8m0", torch.float16, torch.float16, False),       # 6.875 chunks
+            (1, 4097, 11008, None, "e5m2", "ue8m0", torch.bfloat16, torch.bfloat16, True),     # 10.75 chunks, N odd
+            (2, 4096, 11008, 256, "e4m3fn", "f32", torch.bfloat16, torch.float32, False),      # 43 groups of 256
+            (1, 600, 12288, 256, "e5m2", "f32", torch.float16, torch.float32, True),
+            (2, 1030, 14336, None, "e4m3fn", "f32", torch.bfloat16, torch.bfloat16, True),
+            (1, 66, 13824, 256, "e4m3fn", "ue8m0", torch.float16, torch.float16, False)]):     # 13.5 chunks
+        _run(M, N, K, G, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=5000 + i)
+    for K, G in ((5632, None), (11008, 256)):
+        q, s, GG, b = _layer(2050, K, G, "e4m3fn", "f32", True, seed=K)
+        x = torch.randn(1, K, generator=torch.Generator().manual_seed(K + 1)).bfloat16().cuda()
+        outs = []
+        for pair in (1, 0):
+            tune(TFP8_GEMV_PAIR=pair)
+            outs.append(_ext.w8a16(x, q, None, s, b, torch.float32, GG, "e4m3fn"))
+        torch.cuda.synchronize()
+        for y in outs:
+            _check(y, x, q, s, GG, "e4m3fn", b, torch.float32, "gemv", f"pair vs streaming K={K}")
+        assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-5), K
+
+
 def test_quad_gemv_shapes(tune):
     """The 4x4x4-MFMA GEMV, forced for every scale layout it can take and from M = 1: one scale per
     row and K-groups of 64/128/256 (group scales fetched across lanes), f32 and UE8M0 scales, both
