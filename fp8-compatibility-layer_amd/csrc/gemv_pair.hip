@@ -22,14 +22,15 @@ void launch_pair_other(int cpr, int x_dtype, int fmt, int M, int L, bool ue8, co
                        const void* ws, const float* bias, void* y, int ydt, int N, int K, hipStream_t s);
 
 // Runs the pair GEMV if it takes the shape (1 <= M <= pair_max_m(), f16/bf16 x, K % 16 == 0 with
-// ceil(K / 1024) chunks in 2..8, or 11 or 12 for M <= 2, one scale per row or K-groups of 64/128/256 that the
+// K = 2048, 4096, 8192 or ceil(K / 1024) chunks of 3, 5, 6, 7 (or 11, 12 for M <= 2), one scale per row or
+// K-groups of 64/128/256 that the
 // chunks cover, weights below 2^31 bytes, y aligned for the pair store); returns NOT_TAKEN otherwise.
 int run_gemv_pair(const void* x, int x_dtype, int M, int K, const uint8_t* w, int N, const void* ws, int ws_kind,
                   int G, int fmt, const float* bias, void* y, int y_dtype, hipStream_t s) {
     if (M < 1 || M > tune(TUNE_GEMV_PAIR_MAX_M) || M > 4 || x_dtype == TFP8_F32 || !tune(TUNE_GEMV_PAIR))
         return NOT_TAKEN;
     const int cpr = (K + GEMV_CHUNK - 1) / GEMV_CHUNK;
-    const bool here = cpr == 2 || cpr == 4 || cpr == 8;
+    const bool here = (cpr == 2 || cpr == 4 || cpr == 8) && K == cpr * GEMV_CHUNK;   // compile-time K
     if (K % 16 || (!here && !pair_other_cpr(cpr, M)) || (long)N * K >= (1L << 31)) return NOT_TAKEN;
     int L = 0;
     if (G != K) {
@@ -42,11 +43,13 @@ int run_gemv_pair(const void* x, int x_dtype, int M, int K, const uint8_t* w, in
         launch_pair_other(cpr, x_dtype, fmt, M, L, ue8, x, w, ws, bias, y, y_dtype, N, K, s);
         return check_launch("tfp8_gemv (pair)");
     }
+// K known at compile time, except at two activation rows, where the run-time-K form measured faster
+// (C2 M=2: 11.15-11.24 vs 11.41-11.48 us, same box; C1 and C2 M=1 the other way round, 4.44 vs 4.39).
 #define TFP8_PAIR_CPR(XD, F, MT)                                                                          \
     {                                                                                                    \
-        if (cpr == 2) launch_pair_l<XD, F, 2, MT>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);       \
-        else if (cpr == 4) launch_pair_l<XD, F, 4, MT>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);  \
-        else launch_pair_l<XD, F, 8, MT>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);               \
+        if (cpr == 2) launch_pair_l<XD, F, 2, MT, MT != 2>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);       \
+        else if (cpr == 4) launch_pair_l<XD, F, 4, MT, MT != 2>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);  \
+        else launch_pair_l<XD, F, 8, MT, MT != 2>(L, ue8, x, w, ws, bias, y, y_dtype, M, N, K, s);               \
     }
 #define TFP8_PAIR_M(XD, F)                                  \
     {                                                      \

@@ -47,11 +47,14 @@ __device__ __forceinline__ uint32_t group_scale(uint32_t v) {
 // MT activation rows (M = MT, or M < MT with the rows past M reading zeros and not stored).
 // Scale and bias loads are unconditional (a missing value reads out of range as zero): a load
 // under a runtime branch made the compiler wait for it before issuing the weight loads.
-template <int XDT, int FMT, int CPR, int L, bool UE8, int WPB, int MT>
+// EXACT: K == 1024 * CPR, known at compile time (the C1 / C2 shapes: the run-time K arithmetic cost
+// C1 ~0.06 us); otherwise K comes from k_arg and may end inside the last chunk.
+template <int XDT, int FMT, int CPR, int L, bool UE8, int WPB, int MT, bool EXACT>
 __global__ __launch_bounds__(64 * WPB) void gemv_pair_kernel(const void* __restrict__ x, const uint8_t* __restrict__ w,
                                                        const void* __restrict__ ws, const float* __restrict__ bias,
-                                                       void* __restrict__ y, int ydt, int M, int N, int K) {
+                                                       void* __restrict__ y, int ydt, int M, int N, int k_arg) {
     constexpr int KP = CPR * GEMV_CHUNK;                // x row stride in LDS (elements; zeros past K)
+    const int K = EXACT ? KP : k_arg;
     constexpr bool GROUPED = L > 0;
     constexpr int TPB = 64 * WPB;
     constexpr int PPR = KP / 8;                         // 16-byte pieces of x per row
@@ -71,7 +74,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_pair_kernel(const void* __restr
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {                      // piece p: row p / PPR, elements 8 (p % PPR) ..
         const int p = tid + q * TPB, m = p / PPR, kk = (p - m * PPR) * 8;
-        xq[q] = buf_load16(xr, kk < K ? (uint32_t)(m * K + kk) * 2u : BUF_OOB, 0);   // past x / K: zeros
+        if constexpr (EXACT) xq[q] = buf_load16(xr, (uint32_t)p * 16u, 0);                // past x: zeros
+        else xq[q] = buf_load16(xr, kk < K ? (uint32_t)(m * K + kk) * 2u : BUF_OOB, 0);   // past x / K: zeros
     }
 
     // Scales and bias of the pair.  Grouped: lane j*L + i (i < CPR) loads group i*(1024/G) + j.
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_pair_kernel(const void* __restr
     // Every weight load of the pair.
     const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(w, (uint32_t)N * (uint32_t)K);
     const uint32_t lane16 = (uint32_t)lane * 16u;
-    const uint32_t voff_last = lane16 < (uint32_t)(K - (CPR - 1) * GEMV_CHUNK) ? lane16 : BUF_OOB;
+    const uint32_t voff_last = EXACT || lane16 < (uint32_t)(K - (CPR - 1) * GEMV_CHUNK) ? lane16 : BUF_OOB;
     uint4 wv[CPR][2];
 #pragma unroll
     for (int c = 0; c < CPR; ++c)
@@ -208,14 +212,14 @@ __global__ __launch_bounds__(64 * WPB) void gemv_pair_kernel(const void* __restr
 // 4.36, 4 per block 4.63; C2 M=1 (7168 pairs) 4 per block 10.56, 8 per block 10.92; 7, 14 or 16 per
 // block were slower for both (5.3-5.9 and 11.1-12.1).
 
-template <int XDT, int FMT, int CPR, int MT>
+template <int XDT, int FMT, int CPR, int MT, bool EXACT>
 void launch_pair_l(int L, bool ue8, const void* x, const uint8_t* w, const void* ws, const float* bias, void* y,
                    int ydt, int M, int N, int K, hipStream_t s) {
     const int pairs = (N + 1) / 2;
     const int wpb = MT == 1 ? pair_waves_per_block(pairs) : 4;
     const unsigned grid = (unsigned)((pairs + wpb - 1) / wpb);
 #define TFP8_PAIR_W(LV, U, W) \
-    gemv_pair_kernel<XDT, FMT, CPR, LV, U, W, MT><<<grid, 64 * W, 0, s>>>(x, w, ws, bias, y, ydt, M, N, K)
+    gemv_pair_kernel<XDT, FMT, CPR, LV, U, W, MT, EXACT><<<grid, 64 * W, 0, s>>>(x, w, ws, bias, y, ydt, M, N, K)
 #define TFP8_PAIR_U(LV, W) { if (ue8) TFP8_PAIR_W(LV, true, W); else TFP8_PAIR_W(LV, false, W); }
 #define TFP8_PAIR(LV)                                         \
     {                                                         \

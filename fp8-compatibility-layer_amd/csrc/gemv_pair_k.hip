@@ -19,22 +19,22 @@ void launch_pair_other(int cpr, int x_dtype, int fmt, int M, int L, bool ue8, co
 #define TFP8_PAIRK_CPR(XD, F, MT)                                                                          \
     {                                                                                                     \
         switch (cpr) {                                                                                    \
-            case 3: launch_pair_l<XD, F, 3, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
-            case 5: launch_pair_l<XD, F, 5, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
-            case 6: launch_pair_l<XD, F, 6, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
-            case 7: launch_pair_l<XD, F, 7, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
-            case 11: launch_pair_l<XD, F, 11, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;     \
-            default: launch_pair_l<XD, F, 12, MT>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;     \
+            case 3: launch_pair_l<XD, F, 3, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
+            case 5: launch_pair_l<XD, F, 5, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
+            case 6: launch_pair_l<XD, F, 6, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
+            case 7: launch_pair_l<XD, F, 7, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
+            case 11: launch_pair_l<XD, F, 11, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;     \
+            default: launch_pair_l<XD, F, 12, MT, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;     \
         }                                                                                                 \
     }
 // Four activation rows only up to 8 chunks (x of the block within 64 KB of LDS).
 #define TFP8_PAIRK_CPR4(XD, F)                                                                            \
     {                                                                                                     \
         switch (cpr) {                                                                                    \
-            case 3: launch_pair_l<XD, F, 3, 4>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
-            case 5: launch_pair_l<XD, F, 5, 4>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
-            case 6: launch_pair_l<XD, F, 6, 4>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
-            default: launch_pair_l<XD, F, 7, 4>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
+            case 3: launch_pair_l<XD, F, 3, 4, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
+            case 5: launch_pair_l<XD, F, 5, 4, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
+            case 6: launch_pair_l<XD, F, 6, 4, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;        \
+            default: launch_pair_l<XD, F, 7, 4, false>(L, ue8, x, w, ws, bias, y, ydt, M, N, K, s); break;       \
         }                                                                                                 \
     }
 #define TFP8_PAIRK_M(XD, F)                                 \

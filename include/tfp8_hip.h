@@ -107,7 +107,8 @@ int tfp8_dequant(const uint8_t* w, int N, int K, const void* ws, int ws_kind, in
  *
  * M <= 8 runs the GEMV path: the 4x4x4-MFMA GEMV for 3-8 f16/bf16 rows with one scale per row
  * (3-4 rows with K groups of 64, 128 or 256) and K = 2048 or 4096; the row-pair GEMV for 1-4
- * f16/bf16 rows when K / 1024 rounded up is 2 to 8 (11 or 12 for 1-2 rows), G == K or G is 64,
+ * f16/bf16 rows when K is 2048, 4096 or 8192, or K / 1024 rounded up is 3, 5, 6 or 7 (11 or 12 for
+ * 1-2 rows), G == K or G is 64,
  * 128 or 256 (G >= 16 * that chunk count), and N is even for M > 1; otherwise the
  * streaming GEMV up to 3 rows and the matrix-core decode kernel from 4.  M > 8 runs the MFMA
  * GEMM path (the decode kernel up to 16 rows, then the weight-streaming, direct-to-LDS or
