@@ -497,6 +497,27 @@ def test_row_pair_gemv_partial_chunk_shapes(tune):
         assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-5), K
 
 
+def test_row_pair_gemv_chunk_tails(tune):
+    """K across the row-pair GEMV's chunk boundaries: a last chunk of one lane (K = 1024 c + 16),
+    of 3 and 15 lanes, K groups whose last one ends inside the tail, 1 to 4 activation rows, N odd
+    at M = 1 and not a multiple of the block; chunk counts the kernel does not take (9, or 11 at
+    M = 3) go to the other kernels.  Every result against the oracle."""
+    tune(TFP8_GEMV_QUAD=0)
+    for i, (M, N, K, G, fmt, sf) in enumerate([
+            (1, 37, 2064, None, "e4m3fn", "f32"),      # 3 chunks, tail of 1 lane
+            (2, 130, 3120, None, "e5m2", "ue8m0"),     # 4 chunks (not exact): other kernels
+            (4, 66, 4144, None, "e4m3fn", "f32"),      # 5 chunks, tail 3 lanes
+            (3, 262, 5376, 128, "e5m2", "f32"),        # 6 chunks, 42 groups of 128
+            (1, 515, 6400, 256, "e4m3fn", "ue8m0"),    # 7 chunks, 25 groups of 256 (last one in the tail)
+            (2, 98, 7408, None, "e4m3fn", "f32"),      # 8 chunks (not exact): other kernels
+            (1, 45, 8432, None, "e5m2", "f32"),        # 9 chunks: other kernels
+            (2, 1026, 10480, None, "e4m3fn", "ue8m0"), # 11 chunks, tail 15 lanes
+            (3, 64, 10496, 256, "e4m3fn", "f32"),      # 11 chunks at M = 3: other kernels
+            (1, 257, 12032, 256, "e5m2", "ue8m0")]):   # 12 chunks, 47 groups of 256
+        _run(M, N, K, G, torch.float32, fmt=fmt, xdt=torch.bfloat16 if i % 2 else torch.float16, sf=sf,
+             bias=bool(i % 3), seed=6000 + i)
+
+
 def test_quad_gemv_shapes(tune):
     """The 4x4x4-MFMA GEMV, forced for every scale layout it can take and from M = 1: one scale per
     row and K-groups of 64/128/256 (group scales fetched across lanes), f32 and UE8M0 scales, both
