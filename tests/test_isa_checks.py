@@ -6,7 +6,10 @@ the two places where inline assembly steps outside what the compiler can check:
   hazard the compiler cannot see inside the asm, so every DPP source must come from an LDS load
   (or be written at least three instructions earlier);
 * the direct-to-LDS GEMM sets m0 in its `buffer_load ... lds` asm (and declares the clobber); the
-  compiler must not keep anything of its own in m0 in those kernels.
+  compiler must not keep anything of its own in m0 in those kernels;
+* the same GEMM loads its K-group scales with inline-assembly buffer loads into VGPRs, retired by
+  an explicit `s_waitcnt vmcnt`: the compiler does not know those registers fill asynchronously,
+  so no instruction may read, write or copy them before that wait.
 
 CPU only (hipcc cross-compiles for gfx950); skipped when hipcc is absent."""
 import os
@@ -93,3 +96,22 @@ def test_gemm_direct_m0_only_set_by_the_dma_asm(isa):
         for x in ins:
             if re.search(r"\bm0\b", x):
                 assert re.match(r"s_mov_b32 m0, s\d+$", x), f"{name}: compiler use of m0: {x!r}"
+
+
+def test_gemm_direct_scale_loads_untouched_until_their_wait(isa):
+    ks = _kernels(isa["gemm_direct.hip"], "gemm_direct_kernel")
+    checked = 0
+    for name, ins in ks.items():
+        for i, x in enumerate(ins):
+            m = re.match(r"buffer_load_(ubyte|dword) (v\d+), ", x)
+            if not m or " lds" in x:
+                continue
+            reg = m.group(2)
+            for y in ins[i + 1:]:
+                if y.startswith("s_waitcnt") and "vmcnt" in y:
+                    break
+                if y.startswith(("s_cbranch", "s_branch", "s_endpgm")):
+                    break
+                assert not re.search(r"\b%s\b" % reg, y), f"{name}: {reg} of {x!r} used before its wait: {y!r}"
+            checked += 1
+    assert checked >= 16, checked        # the 16 scale loads of a K-group kernel at least
