@@ -195,14 +195,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         boff[i] = (uint32_t)br * (uint32_t)K + (uint32_t)bc * 16u;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t)smem;
-    auto issue = [&](int st) {
-        const uint32_t sa = lds0 + (uint32_t)(st % S) * STAGE;
-        const uint32_t kk = (uint32_t)(kbeg + st * GD_BK);
+    // Loads K step st (K position kk) into the ring slot at LDS offset so.
+    auto issue_at = [&](uint32_t so, uint32_t kk) {
+        const uint32_t sa = lds0 + so;
 #pragma unroll
         for (int i = 0; i < LA; ++i) gd_load_lds(ra, sa + (wave * LA + i) * 1024, aoff[i], kk * 2u);
 #pragma unroll
         for (int i = 0; i < LB; ++i) gd_load_lds(rb, sa + ABYTES + (wave * LB + i) * 1024, boff[i], kk);
     };
+    auto issue = [&](int st) { issue_at((uint32_t)(st % S) * STAGE, (uint32_t)(kbeg + st * GD_BK)); };
 
     // Fragment offsets inside a stage.  Window p (k = 32p .. 32p+31 of the step), half q:
     // activation chunk 4p + 2h + q of row wm*WTM + tm*32 + l32; weight chunk 2p + h of row
@@ -241,8 +242,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
         uint32_t s[SMODE == GD_FOLD ? TN : 1];   // UE8M0 byte of the window's group, per tile; fix()
                                                  // turns it into the f32 scale's bits
     };
-    auto read = [&](int st, int p, Frag& f) {
-        const uint8_t* base = smem + (st % S) * STAGE;
+    // Reads window p of the stage at LDS offset so; g is the window's column of the staged scales
+    // (G % 32 == 0: the window's 32 codes, both lane halves, lie in one group).
+    auto read_at = [&](uint32_t so, int p, int g, Frag& f) {
+        const uint8_t* base = smem + so;
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) f.b[tn] = *(const uint4*)(base + b_rd[p] + tn * 2048);
 #pragma unroll
@@ -250,11 +253,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
 #pragma unroll
             for (int q = 0; q < 2; ++q) f.a[tm][q] = *(const V*)(base + a_rd[p][q] + tm * 4096);
         if constexpr (SMODE == GD_FOLD) {
-            // G % 32 == 0: the window's 32 codes (both lane halves) lie in one group
-            const int g = (kbeg + st * GD_BK + 32 * p) / G - gfirst;
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) f.s[tn] = gd_scales[scale_row(tn) + g];
         }
+    };
+    auto read = [&](int st, int p, Frag& f) {
+        read_at((uint32_t)(st % S) * STAGE, p, SMODE == GD_FOLD ? (kbeg + st * GD_BK + 32 * p) / G - gfirst : 0, f);
     };
     // The scale bytes are converted at the end of the step that read them, after its MFMAs: the
     // wait for the byte then costs nothing, where converting it in read() would wait for the
@@ -374,21 +378,53 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_direct_kernel(
     // the loop, the compiler's wait counts at the merge points had to cover the LDS reads just
     // issued for the next step: lgkmcnt(0) before the last MFMAs of every step.)  The scheduling
     // barriers keep each window's reads ahead of the multiplies that overlap them.
+    // The steady state carries its ring positions and scale column from step to step (a division
+    // or remainder by a run-time G, or by a ring depth that is no power of two, costs a dozen scalar
+    // instructions per use): rso / lso are the LDS offsets of the stages read and loaded next
+    // (t + 1 and t + S - 1), lk the K position of the latter, and gq / gr the staged-scale column of
+    // the next window to read and its position among the G / 32 windows of its group.
+    constexpr uint32_t RING = (uint32_t)S * STAGE;
+    uint32_t rso = (uint32_t)(1 % S) * STAGE, lso = (uint32_t)((S - 1) % S) * STAGE;
+    uint32_t lk = (uint32_t)(kbeg + (S - 1) * GD_BK);
+    const int wpg = SMODE == GD_FOLD ? G / 32 : 1;
+    int gq = 0, gr = 0;
+    if constexpr (SMODE == GD_FOLD) {
+        const int w = kbeg / 32 + 2;                  // first window of step 1
+        gq = w / wpg - gfirst;
+        gr = w % wpg;
+    }
+    auto next_window = [&]() {
+        if constexpr (SMODE == GD_FOLD) {
+            const bool wrap = ++gr == wpg;
+            gq += wrap ? 1 : 0;
+            gr = wrap ? 0 : gr;
+        }
+    };
     auto step_full = [&](int t, Frag& c0, Frag& c1, Frag& n0, Frag& n1) {
         gd_wait_vm_const<(LA + LB) * (S - 3)>();     // stage t + 1 done; t + 2 .. t + S - 2 may be in flight
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        issue(t + S - 1);
-        read(t + 1, 0, n0);
+        issue_at(lso, lk);
+        read_at(rso, 0, gq, n0);
+        next_window();
         __builtin_amdgcn_sched_barrier(0);
         mma(c0);
-        read(t + 1, 1, n1);
+        read_at(rso, 1, gq, n1);
+        next_window();
         __builtin_amdgcn_sched_barrier(0);
         mma(c1);
         fold_group(t);
         fix(n0);
         fix(n1);
+        if constexpr ((RING & (RING - 1)) == 0) {
+            rso = (rso + STAGE) & (RING - 1);
+            lso = (lso + STAGE) & (RING - 1);
+        } else {
+            rso = rso + STAGE == RING ? 0u : rso + STAGE;
+            lso = lso + STAGE == RING ? 0u : lso + STAGE;
+        }
+        lk += GD_BK;
     };
     int t = 0;
     for (; t + 1 < nst - (S - 1); t += 2) {
