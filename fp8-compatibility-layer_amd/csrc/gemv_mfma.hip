@@ -68,8 +68,11 @@ __device__ __forceinline__ uint4 gv_load16(__amdgpu_buffer_rsrc_t r, uint32_t of
                : __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// Two 4-wave blocks per CU at least: the register cap this gives the compiler (C2 M=8 / C3 M=16:
+// 14.84 -> 14.70 / 15.60 -> 15.10 us with the default configuration; 4 waves, 4 chunks in flight,
+// 160 -> 152 VGPRs) also lets the 8-chunk form fit two waves per SIMD (308 -> 248 VGPRs).
 template <typename T, int FMT, int SMODE, int NT, int W, int D, bool TL>
-__global__ __launch_bounds__(64 * W) void gemv_mfma_kernel(const T* __restrict__ x, const float* __restrict__ xs,
+__global__ __launch_bounds__(64 * W, 512 / (64 * W)) void gemv_mfma_kernel(const T* __restrict__ x, const float* __restrict__ xs,
                                                            const uint8_t* __restrict__ w, const void* __restrict__ ws,
                                                            int sk, const float* __restrict__ bias,
                                                            void* __restrict__ y, int ydt, int M, int N, int K, int G,
