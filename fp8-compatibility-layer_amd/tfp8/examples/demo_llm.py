@@ -21,7 +21,7 @@ and the FP8Linear path counters.  Layout choices for the GPU:
     latency figure;
   * on the GPU the decode step runs the work between the FP8 linears as fused ops (llm_ops.hip:
     residual add + RMSNorm, rotary + cache write, split-sequence attention, SiLU * up, and for up
-    to 4 rows the tied head straight from the bf16 embedding), with q/k/v and gate/up each as one
+    to 16 rows the tied head straight from the bf16 embedding), with q/k/v and gate/up each as one
     FP8Linear: about 10 kernels per layer where the PyTorch form of the same step
     (decode_step(fused=False), also the CPU path) launches about 60.
 """
@@ -255,9 +255,9 @@ class Llama(nn.Module):
                 g, u = mlp.gate_proj(y), mlp.up_proj(y)
             r = mlp.down_proj(ops.silu_mul(g, u))
         _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
-        if y.shape[0] <= 4:          # reads the bf16 embedding once (half the bytes of the fp32 copy)
+        if y.shape[0] <= 16:         # reads the bf16 embedding once (half the bytes of the fp32 copy)
             return ops.head(y, self.embed.weight)
-        if self._head32 is None or self._head32.device != y.device:   # more rows: an fp32 GEMM is faster
+        if self._head32 is None or self._head32.device != y.device:   # more rows: an fp32 GEMM
             self._head32 = self.embed.weight.detach().float()
         return F.linear(y.float(), self._head32)
 

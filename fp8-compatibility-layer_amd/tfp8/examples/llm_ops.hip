@@ -236,49 +236,70 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* 
     }
 }
 
+typedef __bf16 hbf16x8 __attribute__((ext_vector_type(8)));
+typedef float hf32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 head_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
 // Tied output head of the decode step: y[b, v] = sum_k float(x[b, k]) * float(w[v, k]) with fp32
-// accumulation, x the normed hidden state (bf16 [NB, K]) and w the bf16 embedding [V, K] -- the
-// products of Llama._head's F.linear(x.float(), embedding.float()), read from the bf16 embedding
-// itself instead of an fp32 copy of it.  Block of 4 waves, 4 embedding rows per wave; x widened
-// into LDS; lane l takes k = 512 it + 8 l .. + 7 (K % 512 == 0).
-template <int NB>
-__global__ __launch_bounds__(256) void head_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                   float* __restrict__ y, int V, int K) {
-    extern __shared__ float xs[];                  // NB * K
-    for (int i = threadIdx.x; i < NB * K; i += 256) xs[i] = bf(x[i]);
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * 4;
-    if (r0 >= V) return;
-    float acc[4][NB];
+// accumulation, x the normed hidden state (bf16 [NB, K], NB <= 16) and w the bf16 embedding [V, K]
+// -- the products of Llama._head's F.linear(x.float(), embedding.float()), read from the bf16
+// embedding itself instead of an fp32 copy of it.  v_mfma_f32_16x16x32_bf16 forms the same
+// products (bf16 x bf16 is exact in fp32) and sums them in fp32 in its own order.  Block: 32
+// embedding rows (two 16-row tiles) and 4 waves splitting K; lane l takes x row l & 15 and row l & 15
+// of each tile at k = 8 (l >> 4) .. + 7 of every 32-wide step (16-byte loads, the MFMA operands as
+// loaded; rows past NB or V read zeros through the buffer resources).  D steps of loads in flight
+// per wave, issued unconditionally (past the wave's range they read zeros), so the loop has no
+// branch for the compiler to wait at.  Requires K % (128 D) == 0.
+template <int D>
+__global__ __launch_bounds__(256) void head_mfma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                        float* __restrict__ y, int NB, int V, int K) {
+    __shared__ hf32x4 red[4][2][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * 32, rows = min(32, V - n0);
+    const int kw = K / 4, nst = kw / 32;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, NB * K * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(w + (size_t)n0 * K), (short)0, rows * K * 2, 0x00020000);
+    const uint32_t base = ((uint32_t)j * (uint32_t)K + (uint32_t)(wave * kw + q * 8)) * 2u;
+    const uint32_t tile1 = 16u * (uint32_t)K * 2u;
+    uint4 xa[D], wa[D], wb[D];
+    auto issue = [&](int d, int st) {
+        const uint32_t off = st < nst ? base + (uint32_t)st * 64u : 0x80000000u;
+        xa[d] = head_load(xr, off);
+        wa[d] = head_load(wr, off);
+        wb[d] = head_load(wr, st < nst ? off + tile1 : 0x80000000u);
+    };
+    hf32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int d = 0; d < D; ++d) issue(d, d);
+    for (int st = 0; st < nst; st += D) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
-    for (int k = lane * 8; k < K; k += 512) {
-        uint4 wv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            wv[r] = r0 + r < V ? *(const uint4*)(w + (size_t)(r0 + r) * K + k) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float4 xa = *(const float4*)(xs + b * K + k), xb = *(const float4*)(xs + b * K + k + 4);
-            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint16_t* wr = (const uint16_t*)&wv[r];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[r][b] = fmaf(xv[j], bf(wr[j]), acc[r][b]);
-            }
+        for (int d = 0; d < D; ++d) {
+            const hbf16x8 a = __builtin_bit_cast(hbf16x8, xa[d]);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(hbf16x8, wa[d]), acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(hbf16x8, wb[d]), acc1, 0, 0, 0);
+            issue(d, st + d + D);
         }
     }
+    // Lane l holds x rows 4 (l >> 4) + r of embedding row l & 15 of each tile; the waves' K ranges
+    // are added in order in LDS.
+    red[wave][0][lane] = acc0;
+    red[wave][1][lane] = acc1;
+    __syncthreads();
+    if (wave >= 2) return;
+    hf32x4 tot = red[0][wave][lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int v = 1; v < 4; ++v) tot += red[v][wave][lane];
+    const int n = n0 + wave * 16 + j;
+    if (n >= V) return;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float t = wave_sum(acc[r][b]);
-            if (lane == 0 && r0 + r < V) y[(size_t)b * V + r0 + r] = t;
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * q + r;
+        if (m < NB) y[(size_t)m * V + n] = tot[r];
+    }
 }
 
 int launched() { return (int)hipGetLastError(); }
@@ -344,25 +365,14 @@ int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int rows, int n, 
 }
 
 
-// rows <= 8, K % 512 == 0, rows * K <= 16384 (x widened into 64 KB of LDS).
+// rows <= 16, K % 512 == 0, V * K * 2 < 2^31.
 int tfp8_llm_head(const void* x, const void* w, float* y, int rows, int V, int K, void* stream) {
-    if (rows < 0 || rows > 8 || V < 0 || K <= 0 || K % 512 || (int64_t)rows * K > 16384 || !x || !w || !y) return -1;
+    if (rows < 0 || rows > 16 || V < 0 || K <= 0 || K % 512 || !x || !w || !y) return -1;
+    if ((int64_t)V * K * 2 >= (1LL << 31)) return -1;
     if (((uintptr_t)x | (uintptr_t)w) % 16) return -1;
     if (rows == 0 || V == 0) return 0;
-    hipStream_t s = (hipStream_t)stream;
-    const unsigned grid = (unsigned)((V + 15) / 16);
-    const size_t lds = (size_t)rows * K * sizeof(float);
-    const uint16_t *xp = (const uint16_t*)x, *wp = (const uint16_t*)w;
-    switch (rows) {
-        case 1: head_kernel<1><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 2: head_kernel<2><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 3: head_kernel<3><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 4: head_kernel<4><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 5: head_kernel<5><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 6: head_kernel<6><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        case 7: head_kernel<7><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-        default: head_kernel<8><<<grid, 256, lds, s>>>(xp, wp, y, V, K); break;
-    }
+    head_mfma_kernel<4><<<(unsigned)((V + 31) / 32), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)x, (const uint16_t*)w, y, rows, V, K);
     return launched();
 }
 

@@ -136,9 +136,9 @@ def silu_mul(g, u):
 
 
 def head(x, weight):
-    """Logits fp32 [..., V] = x (bf16 [..., K], at most 8 rows) times weight (bf16 [V, K])
+    """Logits fp32 [..., V] = x (bf16 [..., K], at most 16 rows) times weight (bf16 [V, K])
     transposed, with fp32 products and sums: F.linear(x.float(), weight.float()) without widening
-    the weight in memory."""
+    the weight in memory (on the matrix cores)."""
     _bf16(x, "x")
     _bf16(weight, "weight")
     V, K = weight.shape

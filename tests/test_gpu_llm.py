@@ -260,7 +260,7 @@ def test_llm_ops_match_pytorch_forms():
 
         # tied head from the bf16 embedding: F.linear of the widened operands, fp32 sums reordered
         emb = (0.02 * torch.randn(1000, d, device="cuda", generator=g)).bfloat16()
-        for rows in (1, 3, 8):
+        for rows in (1, 3, 4, 5, 8, 16):
             xh = torch.randn(rows, 1, d, device="cuda", generator=g).bfloat16()
             got, want = ops.head(xh, emb), torch.nn.functional.linear(xh.float(), emb.float())
             bound = 1e-5 * torch.nn.functional.linear(xh.float().abs(), emb.float().abs())

@@ -349,7 +349,7 @@ def test_example_ops_library_loads_and_validates_without_gpu():
     assert lib.tfp8_llm_attention(a, a, a, a, a, 1, a, 1, 4, 4, 128, 65, 1.0, None) == -1    # S * 64 < L
     assert lib.tfp8_llm_silu_mul(a, a, a, 2, 16, 8, None) == -1        # row stride below the row
     assert lib.tfp8_llm_silu_mul(a, a, a, 0, 16, 16, None) == 0
-    assert lib.tfp8_llm_head(a, a, a, 9, 100, 512, None) == -1           # more than 8 rows
+    assert lib.tfp8_llm_head(a, a, a, 17, 100, 512, None) == -1          # more than 16 rows
     assert lib.tfp8_llm_head(a, a, a, 1, 100, 520, None) == -1           # K % 512
 
 
