@@ -76,10 +76,11 @@ __global__ __launch_bounds__(64 * W, 512 / (64 * W)) void gemv_mfma_kernel(const
                                                            const uint8_t* __restrict__ w, const void* __restrict__ ws,
                                                            int sk, const float* __restrict__ bias,
                                                            void* __restrict__ y, int ydt, int M, int N, int K, int G,
-                                                           int ng, int gshift, int sbytes) {
+                                                           int ng, int gshift, int sbytes, int rb) {
     using Op = GvOp<T>;
     typedef typename Op::V V;
-    constexpr int RB = 16 * NT;                   // weight rows per block
+    // rb weight rows per block: 16 NT, or 8 (one half-used tile: the other rows read zeros through
+    // the weight resource and are not stored) to give a small N twice the blocks
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     f32x4* red = (f32x4*)(smem + sbytes);         // [W][NT][64] wave results
     const int tid = threadIdx.x, lane = tid & 63;
@@ -87,8 +88,8 @@ __global__ __launch_bounds__(64 * W, 512 / (64 * W)) void gemv_mfma_kernel(const
     const int j = lane & 15, q = lane >> 4;
 
     const int nblk = gridDim.x, xcd = blockIdx.x & 7, q8 = nblk >> 3, r8 = nblk & 7;
-    const int n0 = (xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3)) * RB;
-    const int rows = min(RB, N - n0);
+    const int n0 = (xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3)) * rb;
+    const int rows = min(rb, N - n0);
 
     const int cpr = (K + 63) >> 6;                // 64-byte chunks per row
     const int cw = (cpr + W - 1) / W;
@@ -246,15 +247,18 @@ template <typename T, int FMT, int SMODE, int NT, int W, int D>
 static void gm_launch(const void* x, const float* xs, const uint8_t* w, const void* ws, int sk, const float* bias,
                       void* y, int ydt, int M, int N, int K, int G, int ng, int gshift, int sbytes, bool tl,
                       hipStream_t s) {
-    const unsigned grid = (unsigned)((N + 16 * NT - 1) / (16 * NT));
+    // Below N = 4096 one 16-row tile per block would leave CUs idle: 8 rows per block instead
+    // (N=2048, K=5632, the C5 down projection, M=5/8/16: 8.26/9.09/10.81 -> 7.14/8.03/9.75 us).
+    const int rb = NT == 1 && N < 16 * 256 ? 8 : 16 * NT;
+    const unsigned grid = (unsigned)((N + rb - 1) / rb);
     const size_t lds = (size_t)sbytes + (size_t)W * NT * 64 * sizeof(f32x4) + (tl ? (size_t)W * NT * 4096 : 0);
     if (tl) {
         if constexpr (D % 4 == 0)
             gemv_mfma_kernel<T, FMT, SMODE, NT, W, D, true><<<grid, 64 * W, lds, s>>>(
-                (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes);
+                (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, rb);
     } else {
         gemv_mfma_kernel<T, FMT, SMODE, NT, W, D, false><<<grid, 64 * W, lds, s>>>(
-            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes);
+            (const T*)x, xs, w, ws, sk, bias, y, ydt, M, N, K, G, ng, gshift, sbytes, rb);
     }
 }
 

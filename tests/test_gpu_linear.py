@@ -603,11 +603,13 @@ def test_stream_gemm_transposed_loads_identical(M, N, K, G, sf, tune):
 
 @pytest.mark.parametrize("M,N,K,G,sf", [(4, 14336, 4096, 128, "f32"), (8, 4096, 4096, None, "ue8m0"),
                                         (6, 1000, 2048, 32, "ue8m0"), (8, 520, 4096, 64, "f32"),
-                                        (16, 8192, 8192, None, "ue8m0"), (12, 14336, 4096, 128, "f32")])
+                                        (16, 8192, 8192, None, "ue8m0"), (12, 14336, 4096, 128, "f32"),
+                                        (7, 299, 1024, None, "f32"), (16, 2048, 5632, None, "ue8m0")])
 def test_decode_mfma_transposed_loads_identical(M, N, K, G, sf, tune):
     """The decode kernel's transposed weight loads (4 rows x 256 bytes per load, regrouped through
     LDS) feed the matrix cores the same operands in the same order as the direct layout (16 rows x
-    64 bytes per load): the outputs must be bit-identical."""
+    64 bytes per load): the outputs must be bit-identical.  Below N = 4096 a block owns 8 weight
+    rows (half of its MFMA tile reads zeros), N = 299 ends in a partial block."""
     print(f"[linear] decode transposed vs direct M={M} N={N} K={K} G={G} {sf}", flush=True)
     tune(TFP8_GEMV_PAIR=0, TFP8_GEMV_QUAD=0)
     q, s, GG, b = _layer(N, K, G, "e4m3fn", sf, True, M + N)
