@@ -11,8 +11,11 @@ and the FP8Linear path counters.  Layout choices for the GPU:
     head_dim, max_len] and values as [B, heads, max_len, head_dim], so the fused attention reads
     both as they lie (no transposed copy of the keys); the PyTorch forms widen what they read;
   * attention runs in fp32 (scores, causal mask, softmax, values);
-  * the tied output head keeps one fp32 copy of the embedding (the reference re-widens the
-    embedding to fp32 on every call, demo_llm.py:127);
+  * the tied output head computes F.linear(x.float(), embedding.float()) (demo_llm.py:127) from
+    the bf16 embedding itself on the GPU: bf16 x bf16 products are exact in fp32, so a bf16 GEMM
+    with fp32 sums and fp32 output (torch.mm out_dtype) gives it in another summation order; on
+    the CPU, or for other dtypes, one fp32 copy of the embedding is kept (the reference re-widens
+    it on every call);
   * decoding can be replayed from one captured HIP graph (GraphDecoder): the step has static
     shapes -- the position is a device tensor that drives the rotary angles, the KV-cache write and
     the attention mask over the whole (zero-filled) cache -- and the greedy token and the position
@@ -171,10 +174,18 @@ class Llama(nn.Module):
         ang = torch.arange(start, start + T, device=device, dtype=torch.float32)[:, None] * inv[None, :]
         return ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
 
+    def _logits(self, y):
+        """F.linear(y.float(), embedding.float()) for the normed hidden state y [..., dim]."""
+        w = self.embed.weight
+        if y.is_cuda and y.dtype == torch.bfloat16 and w.dtype == torch.bfloat16:
+            flat = torch.mm(y.reshape(-1, y.shape[-1]), w.t(), out_dtype=torch.float32)
+            return flat.reshape(*y.shape[:-1], w.shape[0])
+        if self._head32 is None or self._head32.device != y.device:
+            self._head32 = w.detach().float()
+        return F.linear(y.float(), self._head32)
+
     def _head(self, x):
-        if self._head32 is None or self._head32.device != x.device:
-            self._head32 = self.embed.weight.detach().float()
-        return F.linear(self.norm(x).float(), self._head32)
+        return self._logits(self.norm(x))
 
     def forward(self, ids, cache, start=0):
         """Logits (fp32) for every position of ids [B, T], appending to cache at `start`."""
@@ -255,11 +266,9 @@ class Llama(nn.Module):
                 g, u = mlp.gate_proj(y), mlp.up_proj(y)
             r = mlp.down_proj(ops.silu_mul(g, u))
         _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
-        if y.shape[0] <= 16:         # reads the bf16 embedding once (half the bytes of the fp32 copy)
+        if y.shape[0] <= 16:         # the decode-size head kernel; more rows: the bf16 GEMM
             return ops.head(y, self.embed.weight)
-        if self._head32 is None or self._head32.device != y.device:   # more rows: an fp32 GEMM
-            self._head32 = self.embed.weight.detach().float()
-        return F.linear(y.float(), self._head32)
+        return self._logits(y)
 
 
 def _concat_fp8(mods):
