@@ -499,8 +499,23 @@ constexpr int GD_NCFG = (int)(sizeof(GD_CFGS) / sizeof(GD_CFGS[0]));
 // (128 x 256, 4 stages).
 int gd_min_m() { return tune(TUNE_GEMM_DIRECT_MIN_M); }
 
-GdCfg gd_cfg(int M) {
+// Split of K for a tile grid: slices of whole 64-wide steps until the grid has a block per CU,
+// slices of at least 1024.
+int gd_slices(long tiles, int K) {
+    int s = 1;
+    while (tiles * s < 256 && s < 8 && K / (s * 2) >= 1024) s *= 2;
+    return s;
+}
+
+// Above 128 rows the 128 x 256 tile, or 128 x 128 where the larger tile's grid has no more blocks
+// than half the CUs (the C5 prefill, M=512: N=K=2048 20.4 -> 16.5 us, N=2048 K=5632 29.1 -> 24.5;
+// with more blocks it loses: N=5632 K=2048 28.0 -> 33.5, M=4096 N=K=2048 48.6 -> 62.1).
+GdCfg gd_cfg(int M, int N, int K) {
     int c = M > 128 ? 0 : M > 64 ? 6 : M > 32 ? 7 : 5;
+    if (c == 0) {
+        const long tiles = (long)((M + 127) / 128) * ((N + 255) / 256);
+        if (tiles * gd_slices(tiles, K) <= 128) c = 6;
+    }
     const int f = tune(TUNE_GEMM_DCFG);   // knob TFP8_GEMM_DCFG: index into GD_CFGS
     if (f >= 0 && f < GD_NCFG) c = f;
     return GD_CFGS[c];
@@ -520,11 +535,10 @@ static int gd_mode(int K, int G, int ws_kind, int x16_dtype) {
 // 1024.  Depends on the shape only (the workspace is sized from it).
 static bool gd_split(int M, int N, int K, int* slices, int* slice_len) {
     if (K % GD_BK != 0 || M < gd_min_m() || !tune(TUNE_GEMM_DIRECT)) return false;
-    const GdCfg c = gd_cfg(M);
+    const GdCfg c = gd_cfg(M, N, K);
     if ((long)c.bn * K >= (1L << 31) || (long)c.bm * K * 2 >= (1L << 31)) return false;
     const long tiles = (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    int s = 1;
-    while (tiles * s < 256 && s < 8 && K / (s * 2) >= 1024) s *= 2;
+    int s = gd_slices(tiles, K);
     const int fs = tune(TUNE_GEMM_SPLITK);
     if (fs > 0) s = std::min(fs, 8);
     int len = ((K + s - 1) / s + GD_BK - 1) / GD_BK * GD_BK;
@@ -541,7 +555,7 @@ static bool gd_plan(int M, int N, int K, int G, int ws_kind, int x16_dtype, int*
                     size_t* dyn) {
     const int md = gd_mode(K, G, ws_kind, x16_dtype);
     if (md < 0 || !gd_split(M, N, K, slices, slice_len)) return false;
-    const GdCfg c = gd_cfg(M);
+    const GdCfg c = gd_cfg(M, N, K);
     *mode = md;
     *dyn = 0;
     if (md != GD_CHANNEL) {
@@ -570,7 +584,7 @@ template <typename T, int FMT, int SMODE>
 static void gd_launch(int slices, int slice_len, size_t dyn, const void* x, const float* xs, const uint8_t* w,
                       const void* ws, int sk, const float* bias, void* y, int ydt, int M, int N, int K, int G,
                       float* part, hipStream_t s) {
-    const GdCfg c = gd_cfg(M);
+    const GdCfg c = gd_cfg(M, N, K);
     const dim3 grid(((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn), slices);
 #define GD_K(BM_, BN_, WM_, WN_, S_)                                                                           \
     if (c.bm == BM_ && c.bn == BN_ && c.wm == WM_ && c.wn == WN_ && c.stages == S_) {                          \
@@ -623,7 +637,7 @@ int run_gemm_direct(const void* x16, int x16_dtype, const float* xs, int M, int 
     }
     int rc = check_launch("tfp8_gemm (direct)");
     if (rc || slices <= 1) return rc;
-    const GdCfg c = gd_cfg(M);
+    const GdCfg c = gd_cfg(M, N, K);
     const int ntm = (M + c.bm - 1) / c.bm, ntn = (N + c.bn - 1) / c.bn;
     const int xcw = (ntm * ntn) % 8 == 0 ? gemm_xcd_cols(ntm, ntn, c.bn) : 0;
     splitk_reduce_launch(part, slices, M, N, ws, ws_kind, mode == GD_CHANNEL ? 1 : 0, xs, bias, y, y_dtype, xcw, s);
