@@ -83,11 +83,24 @@ class Attention(nn.Module):
         vc[:, :, start:start + T] = v.transpose(1, 2)
         L = start + T
         rep = self.nh // self.nkv
-        keys_t, vals = kt[:, :, :, :L].float(), vc[:, :, :L].float()         # [B, Hkv, hd, L], [B, Hkv, L, hd]
+        vals = vc[:, :, :L].float()                                           # [B, Hkv, L, hd]
         if rep > 1:
-            keys_t, vals = keys_t.repeat_interleave(rep, 1), vals.repeat_interleave(rep, 1)
-        qf = q.transpose(1, 2).float().contiguous()                          # [B, H, T, hd]
-        scores = torch.matmul(qf, keys_t) / math.sqrt(self.hd)
+            vals = vals.repeat_interleave(rep, 1)
+        if x.is_cuda and q.dtype == torch.bfloat16 and kt.dtype == torch.bfloat16:
+            # q . k of bf16 values: exact products, so a bf16 batched product with fp32 sums and fp32
+            # output equals the fp32 product of the widened operands up to summation order
+            keys_t = kt[:, :, :, :L]
+            if rep > 1:
+                keys_t = keys_t.repeat_interleave(rep, 1)
+            keys_t = keys_t.reshape(B * self.nh, self.hd, L).contiguous()
+            qb = q.transpose(1, 2).reshape(B * self.nh, T, self.hd).contiguous()
+            scores = torch.bmm(qb, keys_t, out_dtype=torch.float32).view(B, self.nh, T, L) / math.sqrt(self.hd)
+        else:
+            keys_t = kt[:, :, :, :L].float()                                  # [B, Hkv, hd, L]
+            if rep > 1:
+                keys_t = keys_t.repeat_interleave(rep, 1)
+            qf = q.transpose(1, 2).float().contiguous()                      # [B, H, T, hd]
+            scores = torch.matmul(qf, keys_t) / math.sqrt(self.hd)
         if T > 1:
             qpos = torch.arange(start, L, device=x.device)[:, None]
             kpos = torch.arange(L, device=x.device)[None, :]
