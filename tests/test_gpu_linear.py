@@ -377,11 +377,13 @@ def test_split_k_workspace_contents_do_not_matter(direct, tune):
     (384, 512, 4096, torch.bfloat16, torch.bfloat16, "e4m3fn", "ue8m0", True, 3),  # uneven split (1408, 1408, 1280)
     (1000, 2048, 1024, torch.float16, torch.float16, "e5m2", "ue8m0", True, 1),
     (300, 512, 512, torch.float32, torch.float32, "e4m3fn", "f32", True, 2),      # fp32 x: f16 prep + row scales
+    (640, 8192, 1024, torch.bfloat16, torch.bfloat16, "e4m3fn", "ue8m0", True, 0),  # 160 blocks of 128 x 256
 ])
 def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, tune):
     """The direct-load GEMM (M > 128, one scale per weight row): rows past M and N inside a tile,
     K of one to three steps (fewer than the LDS ring holds), even and uneven split-K, f16 / bf16 /
-    fp32 activations, both formats, f32 and UE8M0 scales, every output dtype."""
+    fp32 activations, both formats, f32 and UE8M0 scales, every output dtype.  Grids of at most
+    128 blocks of 128 x 256 take 128 x 128 tiles (every case but the last)."""
     if split:
         tune(TFP8_GEMM_SPLITK=split)
     _run(M, N, K, None, out, fmt=fmt, bias=bias, xdt=xdt, sf=sf, seed=M + K)
@@ -394,6 +396,7 @@ def test_direct_gemm_shapes(M, N, K, xdt, out, fmt, sf, bias, split, tune):
     (300, 1024, 3072, 128, "ue8m0", torch.float16, "e4m3fn", 0),   # UE8M0 groups with f16 x: partial sums
     (130, 256, 4096, 128, "f32", torch.bfloat16, "e4m3fn", 0),     # split 8, slices of 4 groups
     (150, 640, 2304, 192, "f32", torch.bfloat16, "e5m2", 5),       # slices of 512 cut groups of 192
+    (200, 512, 1024, 32, "ue8m0", torch.bfloat16, "e5m2", 0),      # folded UE8M0, 128 x 128 tiles above 128 rows
 ])
 def test_direct_gemm_group_scales(M, N, K, G, sf, xdt, fmt, split, tune):
     """K-group scales on the direct-load GEMM: UE8M0 groups folded into the decode (bf16
@@ -404,7 +407,7 @@ def test_direct_gemm_group_scales(M, N, K, G, sf, xdt, fmt, split, tune):
     _run(M, N, K, G, torch.float32, fmt=fmt, xdt=xdt, sf=sf, seed=M + G)
 
 
-@pytest.mark.parametrize("cfg", list(range(1, 8)))
+@pytest.mark.parametrize("cfg", list(range(0, 8)))
 def test_direct_gemm_every_config(cfg, tune):
     """Every direct-load GEMM configuration (block tile 32/64/128 x 128/256, 4 or 8 waves, rings of
     3 to 7 K steps), forced through the library's tuning hooks at small and large M: rows past M
