@@ -255,8 +255,8 @@ class Llama(nn.Module):
 
     def _decode_fused(self, x, cos, sin, cache, pos):
         """The layers and the head of decode_step with llm_ops between the FP8 linears: per layer
-        residual add + RMSNorm, q/k/v projection (one fused FP8Linear), rotary + cache write,
-        attention, o_proj, residual add + RMSNorm, gate/up projection (one fused FP8Linear), SiLU * up,
+        residual add + RMSNorm, q/k/v projection (one fused FP8Linear), rotary + cache write +
+        attention (one op), o_proj, residual add + RMSNorm, gate/up projection (one fused FP8Linear), SiLU * up,
         down_proj (the block's residual adds ride in the next norm)."""
         from tfp8.examples import llm_ops as ops
         H, Hkv, ffn = self.c["n_heads"], self.c["n_kv"], self.c["ffn"]
@@ -270,8 +270,8 @@ class Llama(nn.Module):
                 q, k, v = o[..., :nq], o[..., nq:nq + nk], o[..., nq + nk:]
             else:
                 q, k, v = at.q_proj(y), at.k_proj(y), at.v_proj(y)
-            qf = ops.rope_cache(q, k, v, cos, sin, kt, vc, pos, H, Hkv)
-            x, y = ops.add_rmsnorm(x, at.o_proj(ops.attention(qf, kt, vc, pos, H, Hkv)), n2.weight, n2.eps)
+            o = ops.rope_attention(q, k, v, cos, sin, kt, vc, pos, H, Hkv)
+            x, y = ops.add_rmsnorm(x, at.o_proj(o), n2.weight, n2.eps)
             if gate_up is not None:
                 o = gate_up(y)
                 g, u = o[..., :ffn], o[..., ffn:]

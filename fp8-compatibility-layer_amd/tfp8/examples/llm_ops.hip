@@ -141,18 +141,52 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
 // o[i] = sum exp(s_t - m) v_t[i], stored as part[(bh * S + j) * (HD + 2) + {0: m, 1: l, 2 + i: o[i]}]
 // (an empty chunk stores m = -inf, l = 0, o = 0).  Query head h reads key/value head h / (H / Hkv)
 // (repeat_interleave over heads).
-template <int HD>
+//
+// With ROPE the block also does rope_cache_kernel's work for its head (one kernel instead of two):
+// it rotates its query head from the projection q itself (the same operations, so qs holds the same
+// values), and the block whose chunk holds position *pos rotates the key head and writes it and the
+// value head into the caches before it reads them (blocks of query heads sharing a key head write
+// the same values).  qf is then unused.
+struct RopeArgs {
+    const uint16_t *q, *k, *v;
+    const float *cs, *sn;
+    uint16_t *kt, *vc;
+    int ldq, ldk, ldv;
+};
+
+template <int HD, bool ROPE>
 __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict__ qf, const uint16_t* __restrict__ kt,
                                                         const uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
-                                                        float* __restrict__ part, int H, int Hkv, int L, float sdiv) {
-    constexpr int Q = HD / 4, G = 256 / HD;
+                                                        float* __restrict__ part, int H, int Hkv, int L, float sdiv,
+                                                        RopeArgs ra) {
+    constexpr int Q = HD / 4, G = 256 / HD, HALF = HD / 2;
     __shared__ float qs[HD], dots[4][64], e[64], oacc[256];
     const int bh = blockIdx.x, j = blockIdx.y, S = gridDim.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int b = bh / H, h = bh - b * H, kh = h / (H / Hkv);
     const size_t hb = (size_t)b * Hkv + kh;
-    const int n = (int)min((int64_t)L, max((int64_t)0, *pos + 1));
+    const int64_t p = *pos;
+    const int n = (int)min((int64_t)L, max((int64_t)0, p + 1));
     const int chunk = (n + S - 1) / S, t0 = min(n, j * chunk), cnt = min(n, t0 + chunk) - t0;
-    if (tid < HD) qs[tid] = qf[(size_t)bh * HD + tid];
+    if constexpr (ROPE) {
+        if (tid < HALF) {
+            const float c = ra.cs[tid], sv = ra.sn[tid];
+            const uint16_t* src = ra.q + (size_t)b * ra.ldq + (size_t)h * HD;
+            const float x1 = bf(src[tid]), x2 = bf(src[tid + HALF]);
+            qs[tid] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sv))));
+            qs[tid + HALF] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sv))));
+            if (p >= t0 && p < t0 + cnt) {
+                const uint16_t* ks = ra.k + (size_t)b * ra.ldk + (size_t)kh * HD;
+                const float y1 = bf(ks[tid]), y2 = bf(ks[tid + HALF]);
+                ra.kt[(hb * HD + tid) * L + p] = to_bf(__fsub_rn(__fmul_rn(y1, c), __fmul_rn(y2, sv)));
+                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(__fadd_rn(__fmul_rn(y2, c), __fmul_rn(y1, sv)));
+                const uint16_t* vs = ra.v + (size_t)b * ra.ldv + (size_t)kh * HD;
+                ra.vc[(hb * L + p) * HD + tid] = vs[tid];
+                ra.vc[(hb * L + p) * HD + tid + HALF] = vs[tid + HALF];
+            }
+        }
+    } else {
+        if (tid < HD) qs[tid] = qf[(size_t)bh * HD + tid];
+    }
     __syncthreads();
     if (lane < cnt) {
         const uint16_t* kp = kt + (hb * HD + w * Q) * L + t0 + lane;
@@ -346,8 +380,31 @@ int tfp8_llm_attention(const float* qf, const void* kt, const void* vc, const in
     if (B == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     const uint16_t *kp = (const uint16_t*)kt, *vp = (const uint16_t*)vc;
-    if (hd == 128) attn_part_kernel<128><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv);
-    else attn_part_kernel<64><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv);
+    const RopeArgs none{};
+    if (hd == 128) attn_part_kernel<128, false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
+    else attn_part_kernel<64, false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
+    int rc = launched();
+    if (rc) return rc;
+    attn_combine_kernel<<<B * H, 256, 0, s>>>(part, (uint16_t*)out, hd, S);
+    return launched();
+}
+
+// tfp8_llm_rope_cache followed by tfp8_llm_attention in two kernels instead of three: the same
+// cache contents and the same output bits (no qf buffer).  Arguments as there; a position outside
+// the cache is refused on the host by the caller, as for rope_cache.
+int tfp8_llm_rope_attention(const void* q, const void* k, const void* v, const float* cs, const float* sn, void* kt,
+                            void* vc, const int64_t* pos, float* part, int S, void* out, int B, int H, int Hkv, int hd,
+                            int L, int ldq, int ldk, int ldv, float sdiv, void* stream) {
+    if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || (hd != 64 && hd != 128) || L <= 0) return -1;
+    if (S <= 0 || (int64_t)S * 64 < L || S > 256 || !kt || !vc || !pos || !part || !out) return -1;
+    if (ldq < H * hd || ldk < Hkv * hd || ldv < Hkv * hd || !q || !k || !v || !cs || !sn) return -1;
+    if (B == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    const RopeArgs ra{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)kt,
+                      (uint16_t*)vc, ldq, ldk, ldv};
+    const uint16_t *kp = (const uint16_t*)kt, *vp = (const uint16_t*)vc;
+    if (hd == 128) attn_part_kernel<128, true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
+    else attn_part_kernel<64, true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
     int rc = launched();
     if (rc) return rc;
     attn_combine_kernel<<<B * H, 256, 0, s>>>(part, (uint16_t*)out, hd, S);

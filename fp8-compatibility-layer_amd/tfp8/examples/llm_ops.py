@@ -26,8 +26,9 @@ def library():
         lib.tfp8_llm_attention.argtypes = [p, p, p, p, p, i, p, i, i, i, i, i, f, p]
         lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i, i, i64, p]
         lib.tfp8_llm_head.argtypes = [p, p, p, i, i, i, p]
+        lib.tfp8_llm_rope_attention.argtypes = [p, p, p, p, p, p, p, p, p, i, p, i, i, i, i, i, i, i, i, f, p]
         for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul,
-                   lib.tfp8_llm_head):
+                   lib.tfp8_llm_head, lib.tfp8_llm_rope_attention):
             fn.restype = ctypes.c_int
         _LIB = lib
     return _LIB
@@ -120,6 +121,36 @@ def attention(qf, kt, vc, pos, n_heads, n_kv):
     _check(library().tfp8_llm_attention(qf.data_ptr(), kt.data_ptr(), vc.data_ptr(), pos.data_ptr(), part.data_ptr(), S,
                                         out.data_ptr(), B, n_heads, n_kv, hd, L, float(math.sqrt(hd)), _stream(qf)),
            "attention")
+    return out
+
+
+def rope_attention(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
+    """rope_cache then attention in two kernels instead of three, with the same cache contents and
+    the same output bits: q, k, v bf16 [B, 1, heads * hd] rows (slices of one fused projection
+    taken as they lie), cos / sin fp32 [hd / 2], the bf16 caches kt [B, n_kv, hd, L] /
+    vc [B, n_kv, L, hd] written at pos (int64 [1] on the device); returns bf16 [B, 1, n_heads * hd]."""
+    B, hd, L = q.shape[0], kt.shape[2], kt.shape[3]
+    (bq, ldq), (bk, ldk), (bv, ldv) = _rows(q, n_heads * hd, "q"), _rows(k, n_kv * hd, "k"), _rows(v, n_kv * hd, "v")
+    if not bq == bk == bv == B:
+        raise ValueError("q/k/v rows do not match the batch")
+    if tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
+        raise ValueError(f"cache shapes {tuple(kt.shape)} / {tuple(vc.shape)}")
+    _bf16(kt, "kt")
+    _bf16(vc, "vc")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{n}: contiguous float32 expected")
+    if cos.numel() != hd // 2 or sin.numel() != hd // 2 or pos.dtype != torch.int64 or pos.numel() != 1:
+        raise ValueError("cos/sin need hd / 2 values and pos one int64")
+    S = math.ceil(L / 64)
+    if S > 256:
+        raise ValueError(f"cache of {L} positions: at most {256 * 64}")
+    part = torch.empty(B * n_heads * S * (hd + 2), dtype=torch.float32, device=q.device)
+    out = torch.empty(B, 1, n_heads * hd, dtype=torch.bfloat16, device=q.device)
+    _check(library().tfp8_llm_rope_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                             kt.data_ptr(), vc.data_ptr(), pos.data_ptr(), part.data_ptr(), S,
+                                             out.data_ptr(), B, n_heads, n_kv, hd, L, ldq, ldk, ldv,
+                                             float(math.sqrt(hd)), _stream(q)), "rope_attention")
     return out
 
 

@@ -235,6 +235,7 @@ def test_llm_ops_match_pytorch_forms():
         kt = torch.randn(B, Hkv, hd, L, device="cuda", generator=g).bfloat16()
         vc = torch.randn(B, Hkv, L, hd, device="cuda", generator=g).bfloat16()
         kt2, vc2 = kt.clone(), vc.clone()
+        kt0, vc0 = kt.clone(), vc.clone()           # before any write at pos
         q = torch.randn(B, 1, H * hd, device="cuda", generator=g).bfloat16()
         k = torch.randn(B, 1, Hkv * hd, device="cuda", generator=g).bfloat16()
         v = torch.randn(B, 1, Hkv * hd, device="cuda", generator=g).bfloat16()
@@ -274,6 +275,12 @@ def test_llm_ops_match_pytorch_forms():
         o_ref32 = o_ref32.transpose(1, 2).reshape(B, 1, H * hd)
         err = (o.float() - o_ref32).abs()
         assert (err <= 2.0 ** -8 * o_ref32.abs() + 1e-5).all(), err.max().item()
+
+        # rotary + cache write fused into the attention kernel: the same caches and output bits
+        kt4, vc4 = kt0.clone(), vc0.clone()
+        o4 = ops.rope_attention(fusedo[..., :H * hd], fusedo[..., H * hd:(H + Hkv) * hd], fusedo[..., (H + Hkv) * hd:],
+                                cos.reshape(-1), sin.reshape(-1), kt4, vc4, pos, H, Hkv)
+        assert torch.equal(kt4, kt) and torch.equal(vc4, vc) and torch.equal(o4, o)
 
         # the first position (one cached row) and the last one (every row) of the cache
         for p in (0, L - 1):
