@@ -220,16 +220,18 @@ class Llama(nn.Module):
         if inv is None or inv.device != tok.device:
             inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device=tok.device, dtype=torch.float32) * 2.0 / hd))
             self.__dict__["_rope_inv"] = inv
-        ang = pos.float()[:, None] * inv[None, :]
-        cos, sin = ang.cos(), ang.sin()                                     # [1, hd / 2]
-        x = self.embed(tok)
         if tok.is_cuda if fused is None else fused:
-            logits = self._decode_fused(x, cos.reshape(-1), sin.reshape(-1), cache, pos)
-        else:
-            cos, sin = cos[None, :, None, :], sin[None, :, None, :]
-            for layer, kv in zip(self.layers, cache):
-                x = layer.forward_static(x, cos, sin, kv, pos, kpos)
-            logits = self._head(x)
+            from tfp8.examples import llm_ops as ops
+            x, cos, sin = ops.step_in(tok, pos, inv, self.embed.weight)     # embedding rows, rotary angles
+            logits = self._decode_fused(x, cos, sin, cache, pos)
+            ops.step_out(logits[:, -1], tok, pos)                           # greedy token, pos + 1
+            return logits
+        ang = pos.float()[:, None] * inv[None, :]
+        cos, sin = ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]   # [1, 1, 1, hd / 2]
+        x = self.embed(tok)
+        for layer, kv in zip(self.layers, cache):
+            x = layer.forward_static(x, cos, sin, kv, pos, kpos)
+        logits = self._head(x)
         tok.copy_(greedy(logits[:, -1]))
         pos.add_(1)
         return logits

@@ -336,6 +336,81 @@ __global__ __launch_bounds__(256) void head_mfma_kernel(const uint16_t* __restri
     }
 }
 
+// Start of a decode step (Llama.decode_step's embedding lookup and rotary angles): block b < B copies
+// embedding row tok[b] (bf16 [V, d]) into x[b] (a token outside 0..V-1 gives a zero row); block B
+// computes the angles pos * inv[i] in fp32 and their cosine and sine, as pos.float() * inv, .cos()
+// and .sin() do.
+__global__ __launch_bounds__(256) void step_in_kernel(const int64_t* __restrict__ tok, const int64_t* __restrict__ pos,
+                                                      const float* __restrict__ inv, const uint16_t* __restrict__ emb,
+                                                      uint16_t* __restrict__ x, float* __restrict__ cs,
+                                                      float* __restrict__ sn, int B, int d, int half, int V) {
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (b == B) {
+        const float pf = (float)*pos;
+        for (int i = tid; i < half; i += 256) {
+            const float a = __fmul_rn(pf, inv[i]);
+            cs[i] = cosf(a);
+            sn[i] = sinf(a);
+        }
+        return;
+    }
+    const int64_t t = tok[b];
+    const bool ok = t >= 0 && t < V;
+    const uint4* src = (const uint4*)(emb + (ok ? (size_t)t * d : 0));
+    uint4* dst = (uint4*)(x + (size_t)b * d);
+    for (int i = tid; i < d / 8; i += 256) dst[i] = ok ? src[i] : make_uint4(0, 0, 0, 0);
+}
+
+// (value, index) order of torch.argmax: NaN above everything, then larger values, then the lower
+// index.
+__device__ __forceinline__ bool am_better(float a, int ia, float b, int ib) {
+    const bool na = a != a, nb = b != b;
+    if (na != nb) return na;
+    if (!na && a != b) return a > b;
+    return ia < ib;
+}
+
+// End of a decode step (greedy(), tok.copy_ and pos.add_(1)): block b writes into tok[b] the index
+// of the first maximum of logits row b (V values, rows ld apart); block 0 then advances pos.
+__global__ __launch_bounds__(1024) void step_out_kernel(const float* __restrict__ logits, int V, int64_t ld,
+                                                        int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const float* row = logits + (size_t)b * ld;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = tid; i < V; i += 1024) {
+        const float v = row[i];
+        if (am_better(v, i, best, idx)) {
+            best = v;
+            idx = i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(idx, off);
+        if (am_better(ov, oi, best, idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if (lane == 0) {
+        bv[w] = best;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int j = 1; j < 16; ++j)
+            if (am_better(bv[j], bi[j], best, idx)) {
+                best = bv[j];
+                idx = bi[j];
+            }
+        tok[b] = idx;
+        if (b == 0) *pos += 1;
+    }
+}
+
 int launched() { return (int)hipGetLastError(); }
 
 }  // namespace
@@ -430,6 +505,24 @@ int tfp8_llm_head(const void* x, const void* w, float* y, int rows, int V, int K
     if (rows == 0 || V == 0) return 0;
     head_mfma_kernel<4><<<(unsigned)((V + 31) / 32), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, (const uint16_t*)w, y, rows, V, K);
+    return launched();
+}
+
+// tok / pos int64 on the device, inv fp32 [half], emb bf16 [V, d] (d % 8 == 0, 16-byte aligned), x bf16
+// [B, d], cs / sn fp32 [half].
+int tfp8_llm_step_in(const int64_t* tok, const int64_t* pos, const float* inv, const void* emb, void* x, float* cs,
+                     float* sn, int B, int d, int half, int V, void* stream) {
+    if (B < 0 || d <= 0 || d % 8 || half <= 0 || V <= 0 || !tok || !pos || !inv || !emb || !x || !cs || !sn) return -1;
+    if (((uintptr_t)emb | (uintptr_t)x) % 16) return -1;
+    step_in_kernel<<<B + 1, 256, 0, (hipStream_t)stream>>>(tok, pos, inv, (const uint16_t*)emb, (uint16_t*)x, cs, sn,
+                                                            B, d, half, V);
+    return launched();
+}
+
+// logits fp32, B rows of V values ld apart; tok int64 [B], pos int64 [1] (advanced by one).
+int tfp8_llm_step_out(const float* logits, int B, int V, int64_t ld, int64_t* tok, int64_t* pos, void* stream) {
+    if (B <= 0 || V <= 0 || ld < V || !logits || !tok || !pos) return -1;
+    step_out_kernel<<<B, 1024, 0, (hipStream_t)stream>>>(logits, V, ld, tok, pos);
     return launched();
 }
 

@@ -27,8 +27,10 @@ def library():
         lib.tfp8_llm_silu_mul.argtypes = [p, p, p, i, i, i64, p]
         lib.tfp8_llm_head.argtypes = [p, p, p, i, i, i, p]
         lib.tfp8_llm_rope_attention.argtypes = [p, p, p, p, p, p, p, p, p, i, p, i, i, i, i, i, i, i, i, f, p]
+        lib.tfp8_llm_step_in.argtypes = [p, p, p, p, p, p, p, i, i, i, i, p]
+        lib.tfp8_llm_step_out.argtypes = [p, i, i, i64, p, p, p]
         for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul,
-                   lib.tfp8_llm_head, lib.tfp8_llm_rope_attention):
+                   lib.tfp8_llm_head, lib.tfp8_llm_rope_attention, lib.tfp8_llm_step_in, lib.tfp8_llm_step_out):
             fn.restype = ctypes.c_int
         _LIB = lib
     return _LIB
@@ -179,3 +181,41 @@ def head(x, weight):
     _check(library().tfp8_llm_head(x.data_ptr(), weight.data_ptr(), y.data_ptr(), x.numel() // K, V, K, _stream(x)),
            "head")
     return y
+
+
+def _i64(t, what, n=None):
+    if t.dtype != torch.int64 or not t.is_cuda or not t.is_contiguous() or (n is not None and t.numel() != n):
+        raise ValueError(f"{what}: contiguous int64 CUDA tensor{'' if n is None else f' of {n}'} expected")
+
+
+def step_in(tok, pos, inv, emb):
+    """The start of a decode step in one kernel: (x, cos, sin) with x = the embedding rows of tok
+    (int64 [B, 1]) as bf16 [B, 1, d] (emb bf16 [V, d]; a token outside the vocabulary gives a zero
+    row), and cos / sin fp32 [hd / 2] of the angles pos.float() * inv (pos int64 [1], inv fp32)."""
+    B = tok.shape[0]
+    _i64(tok, "tok", B)
+    _i64(pos, "pos", 1)
+    _bf16(emb, "emb")
+    if inv.dtype != torch.float32 or not inv.is_contiguous():
+        raise ValueError("inv: contiguous float32 expected")
+    V, d = emb.shape
+    half = inv.numel()
+    x = torch.empty(B, 1, d, dtype=torch.bfloat16, device=emb.device)
+    cs = torch.empty(half, dtype=torch.float32, device=emb.device)
+    sn = torch.empty(half, dtype=torch.float32, device=emb.device)
+    _check(library().tfp8_llm_step_in(tok.data_ptr(), pos.data_ptr(), inv.data_ptr(), emb.data_ptr(), x.data_ptr(),
+                                      cs.data_ptr(), sn.data_ptr(), B, d, half, V, _stream(emb)), "step_in")
+    return x, cs, sn
+
+
+def step_out(logits, tok, pos):
+    """The end of a greedy decode step in one kernel: tok[b] = the index of the first maximum of
+    logits[b] (fp32 [B, V], rows contiguous; NaN counts above everything, as in torch.argmax), then
+    pos += 1 -- greedy(logits), tok.copy_ and pos.add_(1)."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits: float32 CUDA tensor [B, V] with contiguous rows expected")
+    B, V = logits.shape
+    _i64(tok, "tok", B)
+    _i64(pos, "pos", 1)
+    _check(library().tfp8_llm_step_out(logits.data_ptr(), B, V, logits.stride(0), tok.data_ptr(), pos.data_ptr(),
+                                       _stream(logits)), "step_out")

@@ -292,6 +292,34 @@ def test_llm_ops_match_pytorch_forms():
             assert ((o.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-5).all(), p
 
 
+def test_step_in_and_step_out_match_pytorch_forms():
+    """The decode step's own start and end as one kernel each, against decode_step's PyTorch ops bit
+    for bit: the embedding rows of the tokens and cos / sin of pos.float() * inv (step_in); the
+    greedy token (first maximum on ties, NaN above everything, as torch.argmax) with the position
+    advanced by one (step_out)."""
+    from tfp8.examples import llm_ops as ops
+    g = torch.Generator("cuda").manual_seed(13)
+    V, d, hd = 1000, 256, 128
+    emb = torch.randn(V, d, device="cuda", generator=g).bfloat16()
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device="cuda", dtype=torch.float32) * 2.0 / hd))
+    for B, p in ((1, 0), (3, 517), (8, 4095)):
+        tok = torch.randint(0, V, (B, 1), device="cuda", generator=g)
+        pos = torch.tensor([p], dtype=torch.long, device="cuda")
+        x, cs, sn = ops.step_in(tok, pos, inv, emb)
+        ang = pos.float()[:, None] * inv[None, :]
+        assert torch.equal(x, torch.nn.functional.embedding(tok, emb))
+        assert torch.equal(cs, ang.cos().reshape(-1)) and torch.equal(sn, ang.sin().reshape(-1)), p
+        logits = torch.randn(B, 1, V, device="cuda", generator=g)
+        if B > 1:
+            logits[1, 0, 10] = logits[1, 0, 900] = logits[1].max() + 1      # tie: the first index wins
+            logits[2, 0, 77] = float("nan")                                  # NaN above everything
+        want = torch.stack([torch.argmax(logits[b, 0]) for b in range(B)]).view(B, 1)
+        ops.step_out(logits[:, -1], tok, pos)
+        assert torch.equal(tok, want) and pos.item() == p + 1, (B, tok.view(-1).tolist(), want.view(-1).tolist())
+        if B > 1:
+            assert tok[1, 0].item() == 10 and tok[2, 0].item() == 77
+
+
 def test_fused_decode_step_matches_pytorch_step():
     """The decode step with the fused ops between the FP8 linears against the same step as PyTorch
     ops (decode_step(fused=False)): the same greedy tokens over 16 steps at B=1 and B=3, and logits
