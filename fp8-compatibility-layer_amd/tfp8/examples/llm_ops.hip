@@ -380,12 +380,37 @@ __global__ __launch_bounds__(1024) void step_out_kernel(const float* __restrict_
     const float* row = logits + (size_t)b * ld;
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = tid; i < V; i += 1024) {
-        const float v = row[i];
+    auto take = [&](float v, int i) {
         if (am_better(v, i, best, idx)) {
             best = v;
             idx = i;
         }
+    };
+    if ((V & 3) == 0 && ((uintptr_t)row & 15) == 0) {
+        // 16-byte loads, 8 per thread in flight before any comparison (the values of a row are
+        // independent: a loop that compares each load before issuing the next waits once per load)
+        const float4* r4 = (const float4*)row;
+        const int n4 = V / 4;
+        for (int base = 0; base < n4; base += 8 * 1024) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i4 = base + u * 1024 + tid;
+                v[u] = i4 < n4 ? r4[i4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = 4 * (base + u * 1024 + tid);
+                if (i < V) {
+                    take(v[u].x, i);
+                    take(v[u].y, i + 1);
+                    take(v[u].z, i + 2);
+                    take(v[u].w, i + 3);
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < V; i += 1024) take(row[i], i);
     }
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(best, off);

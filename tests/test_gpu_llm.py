@@ -318,6 +318,14 @@ def test_step_in_and_step_out_match_pytorch_forms():
         assert torch.equal(tok, want) and pos.item() == p + 1, (B, tok.view(-1).tolist(), want.view(-1).tolist())
         if B > 1:
             assert tok[1, 0].item() == 10 and tok[2, 0].item() == 77
+    # rows whose length is no multiple of 4 (element loads instead of 16-byte ones), ties included
+    for V2 in (999, 4097):
+        logits = torch.randn(2, 1, V2, device="cuda", generator=g)
+        logits[0, 0, V2 - 1] = logits[0, 0, 3] = logits[0].max() + 1
+        tok = torch.zeros(2, 1, dtype=torch.long, device="cuda")
+        pos = torch.zeros(1, dtype=torch.long, device="cuda")
+        ops.step_out(logits[:, -1], tok, pos)
+        assert tok[0, 0].item() == 3 and tok[1, 0].item() == torch.argmax(logits[1, 0]).item() and pos.item() == 1
 
 
 def test_fused_decode_step_matches_pytorch_step():
