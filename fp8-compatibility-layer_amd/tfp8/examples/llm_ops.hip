@@ -234,6 +234,132 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
 // Combines the chunks: o[i] = sum_j o_j[i] e^(m_j - M) / sum_j l_j e^(m_j - M), M = max_j m_j,
 // rounded to bf16 into out [B, H * hd] (the layout o_proj reads).  Block bh, 256 threads: the
 // chunks' (m, l) pairs are staged in LDS with one load each, then thread i < hd adds its column.
+// The same chunk partials for head dimension 128 with 16-byte cache loads (cache length L % 8 == 0,
+// chunks of a multiple of 8 positions, so every 8-position group starts 16-byte aligned and groups
+// past the chunk are not read).  Keys: thread (dim group dd = tid >> 3, position group pg = tid & 7)
+// loads dims 4 dd .. 4 dd + 3 of positions 8 pg .. 8 pg + 7 (four 16-byte loads) and forms their
+// partial dot products; the 32 dim groups are added with shuffles inside a wave, then across the 4
+// waves in LDS.  Values: thread (dims 8 (tid & 15) .. + 7, positions (tid >> 4) + 16 u, u < 4) adds
+// e_t v_t over its positions (four 16-byte loads), then the 16 position groups are added the same
+// way.  Same partial layout and rotary handling as attn_part_kernel; the sums run in another order.
+template <bool ROPE>
+__global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restrict__ qf, const uint16_t* __restrict__ kt,
+                                                          const uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
+                                                          float* __restrict__ part, int H, int Hkv, int L, float sdiv,
+                                                          RopeArgs ra) {
+    constexpr int HD = 128, HALF = 64;
+    __shared__ float qs[HD], kred[4][64], e[64], vred[4][HD];
+    const int bh = blockIdx.x, j = blockIdx.y, S = gridDim.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int b = bh / H, h = bh - b * H, kh = h / (H / Hkv);
+    const size_t hb = (size_t)b * Hkv + kh;
+    const int64_t p = *pos;
+    const int n = (int)min((int64_t)L, max((int64_t)0, p + 1));
+    const int chunk = ((n + S - 1) / S + 7) & ~7, t0 = min(n, j * chunk), cnt = min(n, t0 + chunk) - t0;
+    if constexpr (ROPE) {
+        if (tid < HALF) {
+            const float c = ra.cs[tid], sv = ra.sn[tid];
+            const uint16_t* src = ra.q + (size_t)b * ra.ldq + (size_t)h * HD;
+            const float x1 = bf(src[tid]), x2 = bf(src[tid + HALF]);
+            qs[tid] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sv))));
+            qs[tid + HALF] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sv))));
+            if (p >= t0 && p < t0 + cnt) {
+                const uint16_t* ks = ra.k + (size_t)b * ra.ldk + (size_t)kh * HD;
+                const float y1 = bf(ks[tid]), y2 = bf(ks[tid + HALF]);
+                ra.kt[(hb * HD + tid) * L + p] = to_bf(__fsub_rn(__fmul_rn(y1, c), __fmul_rn(y2, sv)));
+                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(__fadd_rn(__fmul_rn(y2, c), __fmul_rn(y1, sv)));
+                const uint16_t* vs = ra.v + (size_t)b * ra.ldv + (size_t)kh * HD;
+                ra.vc[(hb * L + p) * HD + tid] = vs[tid];
+                ra.vc[(hb * L + p) * HD + tid + HALF] = vs[tid + HALF];
+            }
+        }
+    } else {
+        if (tid < HD) qs[tid] = qf[(size_t)bh * HD + tid];
+    }
+    __syncthreads();
+    // keys: 8 positions x 4 dims per thread
+    const int pg = tid & 7, dd = tid >> 3;
+    float dot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (8 * pg < cnt) {
+        uint4 kv[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) kv[d] = *(const uint4*)(kt + (hb * HD + 4 * dd + d) * L + t0 + 8 * pg);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const float qd = qs[4 * dd + d];
+            const uint32_t wv[4] = {kv[d].x, kv[d].y, kv[d].z, kv[d].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                dot[2 * u] = fmaf(qd, __uint_as_float(wv[u] << 16), dot[2 * u]);
+                dot[2 * u + 1] = fmaf(qd, __uint_as_float(wv[u] & 0xFFFF0000u), dot[2 * u + 1]);
+            }
+        }
+    }
+    // add the 8 dim groups of this wave (lanes 8 apart), then the 4 waves in LDS
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        float v = dot[u];
+        v = __fadd_rn(v, __shfl_xor(v, 8));
+        v = __fadd_rn(v, __shfl_xor(v, 16));
+        v = __fadd_rn(v, __shfl_xor(v, 32));
+        dot[u] = v;
+    }
+    if (lane < 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kred[w][8 * lane + u] = dot[u];
+    }
+    __syncthreads();
+    float m = -INFINITY, l = 0.f;
+    if (w == 0) {
+        const float sv = lane < cnt ? __fdiv_rn(__fadd_rn(__fadd_rn(kred[0][lane], kred[1][lane]),
+                                                          __fadd_rn(kred[2][lane], kred[3][lane])), sdiv)
+                                    : -INFINITY;
+        m = wave_max(sv);
+        const float ev = lane < cnt ? expf(__fsub_rn(sv, m)) : 0.f;
+        e[lane] = ev;
+        l = wave_sum(ev);
+    }
+    __syncthreads();
+    // values: 8 dims x 4 positions per thread
+    const int dg = tid & 15, pp = tid >> 4;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    uint4 vv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int t = pp + 16 * u;
+        vv[u] = t < cnt ? *(const uint4*)(vc + (hb * L + t0 + t) * HD + 8 * dg) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int t = pp + 16 * u;
+        const float et = t < cnt ? e[t] : 0.f;
+        const uint32_t wv[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            acc[2 * c] = fmaf(et, __uint_as_float(wv[c] << 16), acc[2 * c]);
+            acc[2 * c + 1] = fmaf(et, __uint_as_float(wv[c] & 0xFFFF0000u), acc[2 * c + 1]);
+        }
+    }
+    // add the 4 position groups of this wave (lanes 16 apart), then the 4 waves in LDS
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        float v = acc[c];
+        v = __fadd_rn(v, __shfl_xor(v, 16));
+        v = __fadd_rn(v, __shfl_xor(v, 32));
+        acc[c] = v;
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) vred[w][8 * lane + c] = acc[c];
+    }
+    __syncthreads();
+    float* dst = part + ((size_t)bh * S + j) * (HD + 2);
+    if (tid < HD) dst[2 + tid] = __fadd_rn(__fadd_rn(vred[0][tid], vred[1][tid]), __fadd_rn(vred[2][tid], vred[3][tid]));
+    if (tid == 0) {
+        dst[0] = cnt > 0 ? m : -INFINITY;
+        dst[1] = l;
+    }
+}
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, uint16_t* __restrict__ out,
                                                            int hd, int S) {
     __shared__ float mj[256], fj[256], red[4];
@@ -481,7 +607,9 @@ int tfp8_llm_attention(const float* qf, const void* kt, const void* vc, const in
     hipStream_t s = (hipStream_t)stream;
     const uint16_t *kp = (const uint16_t*)kt, *vp = (const uint16_t*)vc;
     const RopeArgs none{};
-    if (hd == 128) attn_part_kernel<128, false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
+    const bool v16 = hd == 128 && L % 8 == 0 && ((uintptr_t)kt | (uintptr_t)vc) % 16 == 0;
+    if (v16) attn_part16_kernel<false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
+    else if (hd == 128) attn_part_kernel<128, false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
     else attn_part_kernel<64, false><<<dim3(B * H, S), 256, 0, s>>>(qf, kp, vp, pos, part, H, Hkv, L, sdiv, none);
     int rc = launched();
     if (rc) return rc;
@@ -503,7 +631,9 @@ int tfp8_llm_rope_attention(const void* q, const void* k, const void* v, const f
     const RopeArgs ra{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)kt,
                       (uint16_t*)vc, ldq, ldk, ldv};
     const uint16_t *kp = (const uint16_t*)kt, *vp = (const uint16_t*)vc;
-    if (hd == 128) attn_part_kernel<128, true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
+    const bool v16 = hd == 128 && L % 8 == 0 && ((uintptr_t)kt | (uintptr_t)vc) % 16 == 0;
+    if (v16) attn_part16_kernel<true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
+    else if (hd == 128) attn_part_kernel<128, true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
     else attn_part_kernel<64, true><<<dim3(B * H, S), 256, 0, s>>>(nullptr, kp, vp, pos, part, H, Hkv, L, sdiv, ra);
     int rc = launched();
     if (rc) return rc;

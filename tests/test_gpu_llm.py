@@ -291,6 +291,25 @@ def test_llm_ops_match_pytorch_forms():
             ref = torch.matmul(torch.softmax(sc, -1), vc.float().repeat_interleave(rep, 1)).transpose(1, 2).reshape(B, 1, H * hd)
             assert ((o.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-5).all(), p
 
+        # a cache length that is a multiple of 8 takes the 16-byte-load attention kernel: positions
+        # that end a chunk inside an 8-position group, one cached row, every row; and rotary + cache
+        # write fused into it against the two ops
+        L2 = 320
+        kt5 = torch.randn(B, Hkv, hd, L2, device="cuda", generator=g).bfloat16()
+        vc5 = torch.randn(B, Hkv, L2, hd, device="cuda", generator=g).bfloat16()
+        for p in (0, 5, 13, 130, 317, L2 - 1):
+            pos.fill_(p)
+            o = ops.attention(qf, kt5, vc5, pos, H, Hkv)
+            sc = torch.matmul(qf.view(B, H, 1, hd), kt5.float().repeat_interleave(rep, 1)) / (hd ** 0.5)
+            sc = sc.masked_fill(torch.arange(L2, device="cuda") > pos, float("-inf"))
+            ref = torch.matmul(torch.softmax(sc, -1), vc5.float().repeat_interleave(rep, 1)).transpose(1, 2).reshape(B, 1, H * hd)
+            assert ((o.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-5).all(), p
+            ka, va, kb, vb = kt5.clone(), vc5.clone(), kt5.clone(), vc5.clone()
+            qa = ops.rope_cache(q, k, v, cos.reshape(-1), sin.reshape(-1), ka, va, pos, H, Hkv)
+            oa = ops.attention(qa, ka, va, pos, H, Hkv)
+            ob = ops.rope_attention(q, k, v, cos.reshape(-1), sin.reshape(-1), kb, vb, pos, H, Hkv)
+            assert torch.equal(ka, kb) and torch.equal(va, vb) and torch.equal(oa, ob), p
+
 
 def test_step_in_and_step_out_match_pytorch_forms():
     """The decode step's own start and end as one kernel each, against decode_step's PyTorch ops bit
