@@ -341,6 +341,38 @@ def read_traffic():
     return None
 
 
+class ReadProbe:
+    """tfp8_read_probe (a read-only streaming kernel) over one buffer, launched like a Layer."""
+
+    def __init__(self, lib, t, blocks, out):
+        self.fn = lib.tfp8_read_probe
+        self.keep = (t, out)
+        self.args = (t.data_ptr(), t.numel() * t.element_size(), out.data_ptr(), blocks)
+
+    def __call__(self, stream):
+        rc = self.fn(*self.args, stream)
+        if rc:
+            raise RuntimeError(f"tfp8_read_probe rc={rc}")
+
+
+def read_probe(layers, steps, warmup):
+    """A plain read-only streaming kernel over the same rotating code buffers the GEMV streams, best
+    of four launch shapes (256 to 2048 blocks of 512 threads): a reference rate for the GEMV's."""
+    import torch
+    from tfp8 import _ext
+    lib = _ext.require()
+    out = torch.empty(2048, dtype=torch.int32, device=layers[0].keep[1].device)
+    best = None
+    for blocks in (256, 512, 1024, 2048):
+        probes = [ReadProbe(lib, l.keep[1], blocks, out) for l in layers]
+        t = sorted(time_layers(probes, steps, warmup) for _ in range(3))[1]
+        nbytes = layers[0].keep[1].numel()
+        gbs = nbytes / t / 1e9
+        if best is None or gbs > best["gbs"]:
+            best = {"gbs": round(gbs, 1), "us": round(t * 1e6, 3), "blocks": blocks, "bytes": nbytes}
+    return best
+
+
 def _point(layers, nbytes, flops, steps, warmup, runs=1):
     """Average launch duration (median of `runs` timed runs) and its roofline figures."""
     ts = sorted(time_layers(layers, steps, warmup) for _ in range(runs))
@@ -394,6 +426,8 @@ def main():
         layers, c2data, meta = make_layers("c2", 1, dev)
         pts["c2_m1"] = _point(layers, c2_bytes(1), 2.0 * 14336 * 4096, a.steps, a.warmup)
         log(f"[bench] C2 M=1: {pts['c2_m1']}")
+        out["read_probe"] = read_probe(layers, a.steps, a.warmup)
+        log(f"[bench] read-only probe over the same code buffers: {out['read_probe']}")
         out["gemv_meta"] = meta
         if not a.no_calls:
             calls["c2_m1"] = forward_call_us(c2data, 1)
@@ -484,6 +518,14 @@ def main():
                             "traffic_source": "profiles/traffic_gemv_c2_m1.txt: rocprofv3 --pmc FETCH_SIZE and "
                                               "WRITE_SIZE of this kernel on an earlier run (not measured in this run)",
                             "kernel_us": g["us"], "algorithmic_bytes": g["algorithmic_bytes"]}
+        rp = out.get("read_probe")
+        if rp:
+            line["read_probe"] = {**rp, "frac_of_peak": round(rp["gbs"] / PEAK_HBM_GBS, 4),
+                                  "gemv_over_probe": round(g["gbs"] / rp["gbs"], 4),
+                                  "sample": "tfp8_read_probe: a plain read-only kernel (each block a contiguous "
+                                            "share, 16 loads of 16 bytes in flight per thread) over the C2 code "
+                                            "buffers the GEMV streams, rotating copies; best of 256/512/1024/2048 "
+                                            "blocks"}
     if "c3_m256" in pts:
         gm = pts["c3_m256"]
         line["gemm_m256"] = {"tflops": gm["tflops"], "kernel_us": gm["us"], "runs_us": gm["runs_us"],

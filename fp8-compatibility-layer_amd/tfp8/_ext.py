@@ -56,6 +56,7 @@ _SIGS = {
     "tfp8_tuning_reset": (None, []),
     "tfp8_w8a8_quantize": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "tfp8_w8a8_gemm": (_I, [_P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I, _I, _P]),
+    "tfp8_read_probe": (_I, [_P, _SZ, _P, _I, _P]),
 }
 
 

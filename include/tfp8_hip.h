@@ -202,6 +202,14 @@ int tfp8_w8a8_gemm(const uint8_t* a, int fmt_a, const void* sa, const uint8_t* b
                    int ue8m0, int mode, int native_fp8, const float* bias, float* c, int M, int N, int K,
                    void* stream);
 
+/* ---------------------------------------------------------------- measurement
+ * No counterpart in the reference: a plain read-only streaming kernel for the measurement harness
+ * (a reference rate beside the GEMV's).  Reads `bytes` (a multiple of 16, 16-byte aligned)
+ * of p with `blocks` blocks of 512 threads and stores each block's XOR of the 32-bit words it read
+ * in out[block] (blocks <= 65536); the XOR over out[] is the XOR of every word of the buffer.
+ */
+int tfp8_read_probe(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

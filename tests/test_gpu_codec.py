@@ -174,3 +174,21 @@ def test_dequant_matches_oracle(fmt, sf, pow2):
     out16 = torch.empty(64, 256, dtype=torch.float16, device="cuda")
     _ext.dequant_into(out16, q, None, s, G, fmt)
     assert torch.equal(out16.cpu(), want.half())
+
+
+def test_read_probe_reads_every_word():
+    """The measurement harness's read-only probe (tfp8_read_probe) reads every 16-byte piece of the
+    buffer: the XOR of its per-block results is the XOR of all 32-bit words, including buffers that
+    are no multiple of the grid's stride and grids with more threads than pieces."""
+    lib = _ext.library()
+    g = torch.Generator().manual_seed(9)
+    for nbytes, blocks in ((1 << 20, 64), (16 * 1007, 256), (48, 16)):
+        print(f"[codec] read probe {nbytes} bytes, {blocks} blocks", flush=True)
+        buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, generator=g).cuda()
+        out = torch.full((blocks,), 7, dtype=torch.int32, device="cuda")
+        rc = lib.tfp8_read_probe(buf.data_ptr(), nbytes, out.data_ptr(), blocks, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, _ext.last_error()
+        want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
+        got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+        assert got == want, (nbytes, blocks)
+    assert lib.tfp8_read_probe(buf.data_ptr(), 20, out.data_ptr(), 1, None) == -1     # not a multiple of 16

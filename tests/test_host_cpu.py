@@ -225,7 +225,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     names = _header_functions()
-    assert len(names) == 18, names
+    assert len(names) == 19, names
     lib = ctypes.CDLL(_ext.lib_path())
     for n in names:
         assert hasattr(lib, n), n
