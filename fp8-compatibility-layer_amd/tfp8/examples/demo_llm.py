@@ -204,9 +204,25 @@ class Llama(nn.Module):
         """Logits (fp32) for every position of ids [B, T], appending to cache at `start`."""
         cos, sin = self._rope(start, ids.shape[1], ids.device)
         x = self.embed(ids)
+        if x.is_cuda and x.dtype == torch.bfloat16:
+            return self._forward_fused(x, cos, sin, cache, start)
         for layer, kv in zip(self.layers, cache):
             x = layer(x, cos, sin, kv, start)
         return self._head(x)
+
+    def _forward_fused(self, x, cos, sin, cache, start):
+        """forward with the residual adds, RMSNorms and SiLU * up as llm_ops (one kernel each, with
+        the PyTorch form's roundings, as in the decode step); each block's residual adds ride in the
+        next norm, attention is Attention.forward."""
+        from tfp8.examples import llm_ops as ops
+        r = None
+        for layer, kv in zip(self.layers, cache):
+            n1, n2, mlp = layer.input_layernorm, layer.post_attention_layernorm, layer.mlp
+            x, y = ops.add_rmsnorm(x, r, n1.weight, n1.eps)
+            x, y = ops.add_rmsnorm(x, layer.self_attn(y, cos, sin, kv, start), n2.weight, n2.eps)
+            r = mlp.down_proj(ops.silu_mul(mlp.gate_proj(y), mlp.up_proj(y)))
+        _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
+        return self._logits(y)
 
     def decode_step(self, tok, cache, pos, kpos, fused=None):
         """One greedy decode step with static shapes and device-resident state (capturable in a
