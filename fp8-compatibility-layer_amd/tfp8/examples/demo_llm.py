@@ -81,32 +81,38 @@ class Attention(nn.Module):
         kt, vc = cache
         kt[:, :, :, start:start + T] = k.permute(0, 2, 3, 1)
         vc[:, :, start:start + T] = v.transpose(1, 2)
+        return self.attend(q.transpose(1, 2), kt, vc, start)
+
+    def attend(self, q, kt, vc, start):
+        """Causal attention of the rotated queries q [B, H, T, hd] (positions start .. start + T - 1)
+        over cache positions 0 .. start + T - 1, then o_proj; returns [B, T, dim] in q's dtype."""
+        B, _, T, _ = q.shape
         L = start + T
         rep = self.nh // self.nkv
         vals = vc[:, :, :L].float()                                           # [B, Hkv, L, hd]
         if rep > 1:
             vals = vals.repeat_interleave(rep, 1)
-        if x.is_cuda and q.dtype == torch.bfloat16 and kt.dtype == torch.bfloat16:
+        if q.is_cuda and q.dtype == torch.bfloat16 and kt.dtype == torch.bfloat16:
             # q . k of bf16 values: exact products, so a bf16 batched product with fp32 sums and fp32
             # output equals the fp32 product of the widened operands up to summation order
             keys_t = kt[:, :, :, :L]
             if rep > 1:
                 keys_t = keys_t.repeat_interleave(rep, 1)
             keys_t = keys_t.reshape(B * self.nh, self.hd, L).contiguous()
-            qb = q.transpose(1, 2).reshape(B * self.nh, T, self.hd).contiguous()
+            qb = q.reshape(B * self.nh, T, self.hd).contiguous()
             scores = torch.bmm(qb, keys_t, out_dtype=torch.float32).view(B, self.nh, T, L) / math.sqrt(self.hd)
         else:
             keys_t = kt[:, :, :, :L].float()                                  # [B, Hkv, hd, L]
             if rep > 1:
                 keys_t = keys_t.repeat_interleave(rep, 1)
-            qf = q.transpose(1, 2).float().contiguous()                      # [B, H, T, hd]
+            qf = q.float().contiguous()                                       # [B, H, T, hd]
             scores = torch.matmul(qf, keys_t) / math.sqrt(self.hd)
         if T > 1:
-            qpos = torch.arange(start, L, device=x.device)[:, None]
-            kpos = torch.arange(L, device=x.device)[None, :]
+            qpos = torch.arange(start, L, device=q.device)[:, None]
+            kpos = torch.arange(L, device=q.device)[None, :]
             scores = scores.masked_fill(kpos > qpos, float("-inf"))
         o = torch.matmul(torch.softmax(scores, -1), vals)                       # [B, H, T, hd]
-        return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(x.dtype))
+        return self.o_proj(o.transpose(1, 2).reshape(B, T, self.nh * self.hd).to(q.dtype))
 
     def forward_static(self, x, cos, sin, cache, pos, kpos):
         """One decode position with static shapes: x [B, 1, d], pos int64 [1] on the device, kpos =
@@ -211,16 +217,33 @@ class Llama(nn.Module):
         return self._head(x)
 
     def _forward_fused(self, x, cos, sin, cache, start):
-        """forward with the residual adds, RMSNorms and SiLU * up as llm_ops (one kernel each, with
-        the PyTorch form's roundings, as in the decode step); each block's residual adds ride in the
-        next norm, attention is Attention.forward."""
+        """forward with the work between the linears as llm_ops (one kernel each, with the PyTorch
+        form's roundings, as in the decode step): residual add + RMSNorm, rotary + cache write
+        (rope_prefill), SiLU * up; q/k/v and gate/up run as one fused FP8Linear each where the
+        layers allow it (the same row products as the separate layers; a GEMM may sum them in
+        another order).  Each block's residual adds ride in the next norm; the causal attention
+        itself is Attention.attend."""
         from tfp8.examples import llm_ops as ops
+        H, Hkv, ffn = self.c["n_heads"], self.c["n_kv"], self.c["ffn"]
+        nq, nk = self.c["dim"], Hkv * (self.c["dim"] // H)
+        cs, sn = cos.contiguous(), sin.contiguous()
         r = None
-        for layer, kv in zip(self.layers, cache):
-            n1, n2, mlp = layer.input_layernorm, layer.post_attention_layernorm, layer.mlp
+        for layer, (kt, vc), (qkv, gate_up) in zip(self.layers, cache, self._fused_projections()):
+            at, mlp, n1, n2 = layer.self_attn, layer.mlp, layer.input_layernorm, layer.post_attention_layernorm
             x, y = ops.add_rmsnorm(x, r, n1.weight, n1.eps)
-            x, y = ops.add_rmsnorm(x, layer.self_attn(y, cos, sin, kv, start), n2.weight, n2.eps)
-            r = mlp.down_proj(ops.silu_mul(mlp.gate_proj(y), mlp.up_proj(y)))
+            if qkv is not None:
+                o = qkv(y)
+                q, k, v = o[..., :nq], o[..., nq:nq + nk], o[..., nq + nk:]
+            else:
+                q, k, v = at.q_proj(y), at.k_proj(y), at.v_proj(y)
+            q = ops.rope_prefill(q, k, v, cs, sn, kt, vc, start, H, Hkv)
+            x, y = ops.add_rmsnorm(x, at.attend(q, kt, vc, start), n2.weight, n2.eps)
+            if gate_up is not None:
+                o = gate_up(y)
+                g, u = o[..., :ffn], o[..., ffn:]
+            else:
+                g, u = mlp.gate_proj(y), mlp.up_proj(y)
+            r = mlp.down_proj(ops.silu_mul(g, u))
         _, y = ops.add_rmsnorm(x, r, self.norm.weight, self.norm.eps)
         return self._logits(y)
 

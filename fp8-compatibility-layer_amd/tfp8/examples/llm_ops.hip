@@ -11,7 +11,17 @@
 #include <math.h>
 #include <stdint.h>
 
+// Every multiply, add and subtract below is rounded on its own, as PyTorch's separate kernels
+// round them: hipcc contracts a * b + c into v_fma_f32 by default (so do HIP's __fmul_rn and
+// __fadd_rn, which are the plain operators), and x1 c - x2 s as fma(x1, c, -x2 s) changes a bf16
+// result now and then.  The multiply-adds that may fuse are written as fmaf.
+#pragma clang fp contract(off)
+
 namespace {
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return a * b; }
+__device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
+__device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
 
 __device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
@@ -24,7 +34,7 @@ __device__ __forceinline__ uint16_t to_bf(float f) {
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+    for (int o = 32; o >= 1; o >>= 1) v = add_rn(v, __shfl_xor(v, o));
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
@@ -38,7 +48,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+    return add_rn(add_rn(red[0], red[1]), add_rn(red[2], red[3]));
 }
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
@@ -71,18 +81,18 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
                 const uint4 ra = *(const uint4*)(r + base + i);
                 const uint16_t* rs = (const uint16_t*)&ra;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) hs[j] = to_bf(__fadd_rn(bf(xs[j]), bf(rs[j])));
+                for (int j = 0; j < 8; ++j) hs[j] = to_bf(add_rn(bf(xs[j]), bf(rs[j])));
                 *(uint4*)(h + base + i) = ha;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 v[c][j] = bf(hs[j]);
-                ss = __fadd_rn(ss, __fmul_rn(v[c][j], v[c][j]));
+                ss = add_rn(ss, mul_rn(v[c][j], v[c][j]));
             }
         }
     }
     const float ms = __fdiv_rn(block_sum(ss, red), (float)d);
-    const float inv = rsqrtf(__fadd_rn(ms, eps));
+    const float inv = rsqrtf(add_rn(ms, eps));
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int i = (c * 256 + (int)threadIdx.x) * 8;
@@ -92,7 +102,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
             uint4 ya;
             uint16_t* ys = (uint16_t*)&ya;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ys[j] = to_bf(__fmul_rn(__fmul_rn(v[c][j], inv), bf(ws[j])));
+            for (int j = 0; j < 8; ++j) ys[j] = to_bf(mul_rn(mul_rn(v[c][j], inv), bf(ws[j])));
             *(uint4*)(y + base + i) = ya;
         }
     }
@@ -116,8 +126,8 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
         const uint16_t* src = q + (size_t)b * ldq + (size_t)head * hd;
         const float x1 = bf(src[i]), x2 = bf(src[i + half]);
         float* dst = qf + ((size_t)b * H + head) * hd;
-        dst[i] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))));
-        dst[i + half] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s))));
+        dst[i] = bf(to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s))));
+        dst[i + half] = bf(to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s))));
         return;
     }
     const int64_t p = *pos;
@@ -126,9 +136,41 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
     const size_t hb = (size_t)b * Hkv + kh;
     const uint16_t* src = k + (size_t)b * ldk + (size_t)kh * hd;
     const float x1 = bf(src[i]), x2 = bf(src[i + half]);
-    kt[(hb * hd + i) * L + p] = to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
-    kt[(hb * hd + i + half) * L + p] = to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s)));
+    kt[(hb * hd + i) * L + p] = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
+    kt[(hb * hd + i + half) * L + p] = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
     const uint16_t* vs = v + (size_t)b * ldv + (size_t)kh * hd;
+    vc[(hb * L + p) * hd + i] = vs[i];
+    vc[(hb * L + p) * hd + i + half] = vs[i + half];
+}
+
+// The prefill's rotary embedding and cache write (Attention.forward: _rotary of q and k, then the
+// cache slices at start .. start + T - 1): block (head, b * T + t), hd / 2 threads, cos / sin fp32
+// [T, hd / 2].  Query heads write the rotated bf16 q into qo [B, H, T, hd] (the layout of the score
+// product's left operand); key heads write the rotated k into kt [B, Hkv, hd, L] and the value head
+// into vc [B, Hkv, L, hd] at position start + t.  The same operations as rope_cache_kernel, so the
+// same bits as the PyTorch form.
+__global__ void rope_prefill_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                    const uint16_t* __restrict__ v, const float* __restrict__ cs,
+                                    const float* __restrict__ sn, uint16_t* __restrict__ qo, uint16_t* __restrict__ kt,
+                                    uint16_t* __restrict__ vc, int start, int T, int H, int Hkv, int hd, int L,
+                                    int ldq, int ldk, int ldv) {
+    const int head = blockIdx.x, bt = blockIdx.y, b = bt / T, t = bt - b * T, i = threadIdx.x, half = hd / 2;
+    const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+    if (head < H) {
+        const uint16_t* src = q + (size_t)bt * ldq + (size_t)head * hd;
+        const float x1 = bf(src[i]), x2 = bf(src[i + half]);
+        uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
+        dst[i] = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
+        dst[i + half] = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
+        return;
+    }
+    const int kh = head - H, p = start + t;
+    const size_t hb = (size_t)b * Hkv + kh;
+    const uint16_t* src = k + (size_t)bt * ldk + (size_t)kh * hd;
+    const float x1 = bf(src[i]), x2 = bf(src[i + half]);
+    kt[(hb * hd + i) * L + p] = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
+    kt[(hb * hd + i + half) * L + p] = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
+    const uint16_t* vs = v + (size_t)bt * ldv + (size_t)kh * hd;
     vc[(hb * L + p) * hd + i] = vs[i];
     vc[(hb * L + p) * hd + i + half] = vs[i + half];
 }
@@ -172,13 +214,13 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
             const float c = ra.cs[tid], sv = ra.sn[tid];
             const uint16_t* src = ra.q + (size_t)b * ra.ldq + (size_t)h * HD;
             const float x1 = bf(src[tid]), x2 = bf(src[tid + HALF]);
-            qs[tid] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sv))));
-            qs[tid + HALF] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sv))));
+            qs[tid] = bf(to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, sv))));
+            qs[tid + HALF] = bf(to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, sv))));
             if (p >= t0 && p < t0 + cnt) {
                 const uint16_t* ks = ra.k + (size_t)b * ra.ldk + (size_t)kh * HD;
                 const float y1 = bf(ks[tid]), y2 = bf(ks[tid + HALF]);
-                ra.kt[(hb * HD + tid) * L + p] = to_bf(__fsub_rn(__fmul_rn(y1, c), __fmul_rn(y2, sv)));
-                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(__fadd_rn(__fmul_rn(y2, c), __fmul_rn(y1, sv)));
+                ra.kt[(hb * HD + tid) * L + p] = to_bf(sub_rn(mul_rn(y1, c), mul_rn(y2, sv)));
+                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(add_rn(mul_rn(y2, c), mul_rn(y1, sv)));
                 const uint16_t* vs = ra.v + (size_t)b * ra.ldv + (size_t)kh * HD;
                 ra.vc[(hb * L + p) * HD + tid] = vs[tid];
                 ra.vc[(hb * L + p) * HD + tid + HALF] = vs[tid + HALF];
@@ -201,11 +243,11 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
     __syncthreads();
     float m = -INFINITY, l = 0.f;
     if (w == 0) {
-        const float sv = lane < cnt ? __fdiv_rn(__fadd_rn(__fadd_rn(dots[0][lane], dots[1][lane]),
-                                                          __fadd_rn(dots[2][lane], dots[3][lane])), sdiv)
+        const float sv = lane < cnt ? __fdiv_rn(add_rn(add_rn(dots[0][lane], dots[1][lane]),
+                                                          add_rn(dots[2][lane], dots[3][lane])), sdiv)
                                     : -INFINITY;
         m = wave_max(sv);
-        const float ev = lane < cnt ? expf(__fsub_rn(sv, m)) : 0.f;
+        const float ev = lane < cnt ? expf(sub_rn(sv, m)) : 0.f;
         e[lane] = ev;
         l = wave_sum(ev);
     }
@@ -222,7 +264,7 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const float* __restrict_
     if (tid < HD) {
         float o = oacc[tid];
 #pragma unroll
-        for (int gg = 1; gg < G; ++gg) o = __fadd_rn(o, oacc[gg * HD + tid]);
+        for (int gg = 1; gg < G; ++gg) o = add_rn(o, oacc[gg * HD + tid]);
         out[2 + tid] = o;
     }
     if (tid == 0) {
@@ -260,13 +302,13 @@ __global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restric
             const float c = ra.cs[tid], sv = ra.sn[tid];
             const uint16_t* src = ra.q + (size_t)b * ra.ldq + (size_t)h * HD;
             const float x1 = bf(src[tid]), x2 = bf(src[tid + HALF]);
-            qs[tid] = bf(to_bf(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sv))));
-            qs[tid + HALF] = bf(to_bf(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, sv))));
+            qs[tid] = bf(to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, sv))));
+            qs[tid + HALF] = bf(to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, sv))));
             if (p >= t0 && p < t0 + cnt) {
                 const uint16_t* ks = ra.k + (size_t)b * ra.ldk + (size_t)kh * HD;
                 const float y1 = bf(ks[tid]), y2 = bf(ks[tid + HALF]);
-                ra.kt[(hb * HD + tid) * L + p] = to_bf(__fsub_rn(__fmul_rn(y1, c), __fmul_rn(y2, sv)));
-                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(__fadd_rn(__fmul_rn(y2, c), __fmul_rn(y1, sv)));
+                ra.kt[(hb * HD + tid) * L + p] = to_bf(sub_rn(mul_rn(y1, c), mul_rn(y2, sv)));
+                ra.kt[(hb * HD + tid + HALF) * L + p] = to_bf(add_rn(mul_rn(y2, c), mul_rn(y1, sv)));
                 const uint16_t* vs = ra.v + (size_t)b * ra.ldv + (size_t)kh * HD;
                 ra.vc[(hb * L + p) * HD + tid] = vs[tid];
                 ra.vc[(hb * L + p) * HD + tid + HALF] = vs[tid + HALF];
@@ -298,9 +340,9 @@ __global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restric
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         float v = dot[u];
-        v = __fadd_rn(v, __shfl_xor(v, 8));
-        v = __fadd_rn(v, __shfl_xor(v, 16));
-        v = __fadd_rn(v, __shfl_xor(v, 32));
+        v = add_rn(v, __shfl_xor(v, 8));
+        v = add_rn(v, __shfl_xor(v, 16));
+        v = add_rn(v, __shfl_xor(v, 32));
         dot[u] = v;
     }
     if (lane < 8) {
@@ -310,11 +352,11 @@ __global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restric
     __syncthreads();
     float m = -INFINITY, l = 0.f;
     if (w == 0) {
-        const float sv = lane < cnt ? __fdiv_rn(__fadd_rn(__fadd_rn(kred[0][lane], kred[1][lane]),
-                                                          __fadd_rn(kred[2][lane], kred[3][lane])), sdiv)
+        const float sv = lane < cnt ? __fdiv_rn(add_rn(add_rn(kred[0][lane], kred[1][lane]),
+                                                          add_rn(kred[2][lane], kred[3][lane])), sdiv)
                                     : -INFINITY;
         m = wave_max(sv);
-        const float ev = lane < cnt ? expf(__fsub_rn(sv, m)) : 0.f;
+        const float ev = lane < cnt ? expf(sub_rn(sv, m)) : 0.f;
         e[lane] = ev;
         l = wave_sum(ev);
     }
@@ -343,8 +385,8 @@ __global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restric
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         float v = acc[c];
-        v = __fadd_rn(v, __shfl_xor(v, 16));
-        v = __fadd_rn(v, __shfl_xor(v, 32));
+        v = add_rn(v, __shfl_xor(v, 16));
+        v = add_rn(v, __shfl_xor(v, 32));
         acc[c] = v;
     }
     if (lane < 16) {
@@ -353,7 +395,7 @@ __global__ __launch_bounds__(256) void attn_part16_kernel(const float* __restric
     }
     __syncthreads();
     float* dst = part + ((size_t)bh * S + j) * (HD + 2);
-    if (tid < HD) dst[2 + tid] = __fadd_rn(__fadd_rn(vred[0][tid], vred[1][tid]), __fadd_rn(vred[2][tid], vred[3][tid]));
+    if (tid < HD) dst[2 + tid] = add_rn(add_rn(vred[0][tid], vred[1][tid]), add_rn(vred[2][tid], vred[3][tid]));
     if (tid == 0) {
         dst[0] = cnt > 0 ? m : -INFINITY;
         dst[1] = l;
@@ -368,7 +410,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     const float mv = tid < S ? p[(size_t)tid * (hd + 2)] : -INFINITY;
     const float lv = tid < S ? p[(size_t)tid * (hd + 2) + 1] : 0.f;
     const float M = block_max(mv, red);
-    const float f = mv == -INFINITY ? 0.f : expf(__fsub_rn(mv, M));
+    const float f = mv == -INFINITY ? 0.f : expf(sub_rn(mv, M));
     mj[tid] = lv;
     fj[tid] = f;
     __syncthreads();
@@ -391,8 +433,8 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* 
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = e / n, i = r * ld + (e - r * n);
         const float x = bf(g[i]);
-        const float sv = bf(to_bf(__fdiv_rn(x, __fadd_rn(1.f, expf(-x)))));
-        out[e] = to_bf(__fmul_rn(sv, bf(u[i])));
+        const float sv = bf(to_bf(__fdiv_rn(x, add_rn(1.f, expf(-x)))));
+        out[e] = to_bf(mul_rn(sv, bf(u[i])));
     }
 }
 
@@ -474,7 +516,7 @@ __global__ __launch_bounds__(256) void step_in_kernel(const int64_t* __restrict_
     if (b == B) {
         const float pf = (float)*pos;
         for (int i = tid; i < half; i += 256) {
-            const float a = __fmul_rn(pf, inv[i]);
+            const float a = mul_rn(pf, inv[i]);
             cs[i] = cosf(a);
             sn[i] = sinf(a);
         }
@@ -614,6 +656,22 @@ int tfp8_llm_attention(const float* qf, const void* kt, const void* vc, const in
     int rc = launched();
     if (rc) return rc;
     attn_combine_kernel<<<B * H, 256, 0, s>>>(part, (uint16_t*)out, hd, S);
+    return launched();
+}
+
+// Rows of q / k / v: B * T, row r = b * T + t, ldq / ldk / ldv elements apart; 0 <= start and
+// start + T <= L.
+int tfp8_llm_rope_prefill(const void* q, const void* k, const void* v, const float* cs, const float* sn, void* qo,
+                          void* kt, void* vc, int start, int B, int T, int H, int Hkv, int hd, int L, int ldq, int ldk,
+                          int ldv, void* stream) {
+    if (B < 0 || T < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 512 || L <= 0) return -1;
+    if (start < 0 || (int64_t)start + T > L || ldq < H * hd || ldk < Hkv * hd || ldv < Hkv * hd) return -1;
+    if (!q || !k || !v || !cs || !sn || !qo || !kt || !vc) return -1;
+    if (B == 0 || T == 0) return 0;
+    if ((int64_t)B * T > 65535) return -1;                    // gridDim.y
+    rope_prefill_kernel<<<dim3(H + Hkv, B * T), hd / 2, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)qo, (uint16_t*)kt,
+        (uint16_t*)vc, start, T, H, Hkv, hd, L, ldq, ldk, ldv);
     return launched();
 }
 

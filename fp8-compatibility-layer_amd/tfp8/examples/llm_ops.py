@@ -29,6 +29,7 @@ def library():
         lib.tfp8_llm_rope_attention.argtypes = [p, p, p, p, p, p, p, p, p, i, p, i, i, i, i, i, i, i, i, f, p]
         lib.tfp8_llm_step_in.argtypes = [p, p, p, p, p, p, p, i, i, i, i, p]
         lib.tfp8_llm_step_out.argtypes = [p, i, i, i64, p, p, p]
+        lib.tfp8_llm_rope_prefill.argtypes = [p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, i, i, p]
         for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul,
                    lib.tfp8_llm_head, lib.tfp8_llm_rope_attention, lib.tfp8_llm_step_in, lib.tfp8_llm_step_out):
             fn.restype = ctypes.c_int
@@ -154,6 +155,32 @@ def rope_attention(q, k, v, cos, sin, kt, vc, pos, n_heads, n_kv):
                                              out.data_ptr(), B, n_heads, n_kv, hd, L, ldq, ldk, ldv,
                                              float(math.sqrt(hd)), _stream(q)), "rope_attention")
     return out
+
+
+def rope_prefill(q, k, v, cos, sin, kt, vc, start, n_heads, n_kv):
+    """Rotary embedding of T positions' q, k (bf16 [B, T, heads * hd], rows contiguous: column slices
+    of one fused projection are taken as they lie) with cos / sin (fp32, T * hd / 2 values, position
+    major), k and v written into the bf16 caches kt [B, n_kv, hd, L] / vc [B, n_kv, L, hd] at
+    positions start .. start + T - 1 (a host int); returns the rotated q as bf16 [B, n_heads, T, hd]."""
+    B, T = q.shape[0], q.shape[1]
+    hd, L = kt.shape[2], kt.shape[3]
+    (bq, ldq), (bk, ldk), (bv, ldv) = _rows(q, n_heads * hd, "q"), _rows(k, n_kv * hd, "k"), _rows(v, n_kv * hd, "v")
+    if q.dim() != 3 or not bq == bk == bv == B * T:
+        raise ValueError("q/k/v rows do not match [B, T]")
+    if tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
+        raise ValueError(f"cache shapes {tuple(kt.shape)} / {tuple(vc.shape)}")
+    _bf16(kt, "kt")
+    _bf16(vc, "vc")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != T * (hd // 2):
+            raise ValueError(f"{n}: contiguous float32 of T * hd / 2 values expected")
+    if not 0 <= start <= L - T:
+        raise ValueError(f"positions {start} .. {start + T - 1} outside a cache of {L}")
+    qo = torch.empty(B, n_heads, T, hd, dtype=torch.bfloat16, device=q.device)
+    _check(library().tfp8_llm_rope_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                           qo.data_ptr(), kt.data_ptr(), vc.data_ptr(), int(start), B, T, n_heads,
+                                           n_kv, hd, L, ldq, ldk, ldv, _stream(q)), "rope_prefill")
+    return qo
 
 
 def silu_mul(g, u):

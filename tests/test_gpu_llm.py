@@ -311,6 +311,34 @@ def test_llm_ops_match_pytorch_forms():
             assert torch.equal(ka, kb) and torch.equal(va, vb) and torch.equal(oa, ob), p
 
 
+def test_rope_prefill_matches_pytorch_form():
+    """rope_prefill (the prefill's rotary + cache write, one kernel) against Attention.forward's
+    PyTorch form bit for bit: the rotated q in [B, H, T, hd], the rotated k and the v at cache
+    positions start .. start + T - 1, every other cache position untouched; also from column slices
+    of one fused projection output, with grouped and ungrouped heads and two head sizes."""
+    from tfp8.examples import llm_ops as ops
+    g = torch.Generator("cuda").manual_seed(13)
+    for B, T, start, L, H, Hkv, hd in ((2, 37, 5, 64, 8, 4, 128), (1, 512, 0, 512, 16, 16, 128),
+                                       (3, 1, 90, 100, 4, 2, 64)):
+        print(f"[rope_prefill] B={B} T={T} start={start} L={L} H={H} Hkv={Hkv} hd={hd}", flush=True)
+        qkv = torch.randn(B, T, (H + 2 * Hkv) * hd, device="cuda", generator=g).bfloat16()
+        q, k, v = qkv[..., :H * hd], qkv[..., H * hd:(H + Hkv) * hd], qkv[..., (H + Hkv) * hd:]
+        kt = torch.randn(B, Hkv, hd, L, device="cuda", generator=g).bfloat16()
+        vc = torch.randn(B, Hkv, L, hd, device="cuda", generator=g).bfloat16()
+        kt2, vc2 = kt.clone(), vc.clone()
+        inv = 1.0 / (10000.0 ** (torch.arange(0, hd // 2, device="cuda", dtype=torch.float32) * 2.0 / hd))
+        ang = torch.arange(start, start + T, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
+        c4, s4 = ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
+        with torch.no_grad():
+            qo = ops.rope_prefill(q, k, v, c4.contiguous(), s4.contiguous(), kt, vc, start, H, Hkv)
+            q_ref = demo_llm._rotary(q.reshape(B, T, H, hd), c4, s4).transpose(1, 2)
+            k_ref = demo_llm._rotary(k.reshape(B, T, Hkv, hd), c4, s4)
+            kt2[:, :, :, start:start + T] = k_ref.permute(0, 2, 3, 1)
+            vc2[:, :, start:start + T] = v.reshape(B, T, Hkv, hd).transpose(1, 2)
+        assert qo.shape == (B, H, T, hd) and torch.equal(qo, q_ref)
+        assert torch.equal(kt, kt2) and torch.equal(vc, vc2)
+
+
 def test_step_in_and_step_out_match_pytorch_forms():
     """The decode step's own start and end as one kernel each, against decode_step's PyTorch ops bit
     for bit: the embedding rows of the tokens and cos / sin of pos.float() * inv (step_in); the
