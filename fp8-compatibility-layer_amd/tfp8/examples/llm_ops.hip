@@ -144,35 +144,50 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
 }
 
 // The prefill's rotary embedding and cache write (Attention.forward: _rotary of q and k, then the
-// cache slices at start .. start + T - 1): block (head, b * T + t), hd / 2 threads, cos / sin fp32
-// [T, hd / 2].  Query heads write the rotated bf16 q into qo [B, H, T, hd] (the layout of the score
-// product's left operand); key heads write the rotated k into kt [B, Hkv, hd, L] and the value head
-// into vc [B, Hkv, L, hd] at position start + t.  The same operations as rope_cache_kernel, so the
-// same bits as the PyTorch form.
-__global__ void rope_prefill_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                    const uint16_t* __restrict__ v, const float* __restrict__ cs,
-                                    const float* __restrict__ sn, uint16_t* __restrict__ qo, uint16_t* __restrict__ kt,
-                                    uint16_t* __restrict__ vc, int start, int T, int H, int Hkv, int hd, int L,
-                                    int ldq, int ldk, int ldv) {
-    const int head = blockIdx.x, bt = blockIdx.y, b = bt / T, t = bt - b * T, i = threadIdx.x, half = hd / 2;
-    const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
-    if (head < H) {
-        const uint16_t* src = q + (size_t)bt * ldq + (size_t)head * hd;
-        const float x1 = bf(src[i]), x2 = bf(src[i + half]);
-        uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
-        dst[i] = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
-        dst[i + half] = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
-        return;
-    }
-    const int kh = head - H, p = start + t;
+// cache slices at start .. start + T - 1).  Block (head, b * nt + tile): RP_T positions of one head,
+// 256 threads, cos / sin fp32 [T, hd / 2].  Query heads write the rotated bf16 q into qo [B, H, T, hd]
+// (the layout of the score product's left operand).  Key heads stage their rotated tile in LDS as
+// [hd][RP_T] and write every row of kt [B, Hkv, hd, L] as RP_T contiguous positions (a position per
+// thread would scatter 2-byte stores L elements apart); the value head goes straight to vc [B, Hkv,
+// L, hd] rows.  The same operations as rope_cache_kernel, so the same bits as the PyTorch form.
+constexpr int RP_T = 64;
+__global__ __launch_bounds__(256) void rope_prefill_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                           const uint16_t* __restrict__ v, const float* __restrict__ cs,
+                                                           const float* __restrict__ sn, uint16_t* __restrict__ qo,
+                                                           uint16_t* __restrict__ kt, uint16_t* __restrict__ vc, int start,
+                                                           int T, int H, int Hkv, int hd, int L, int ldq, int ldk, int ldv) {
+    extern __shared__ uint16_t tile[];                        // [hd][RP_T + 2]
+    const int nt = (T + RP_T - 1) / RP_T, head = blockIdx.x, b = blockIdx.y / nt;
+    const int t0 = (blockIdx.y - b * nt) * RP_T, cnt = min(RP_T, T - t0), half = hd / 2;
+    const bool is_q = head < H;
+    const int kh = head - H;
     const size_t hb = (size_t)b * Hkv + kh;
-    const uint16_t* src = k + (size_t)bt * ldk + (size_t)kh * hd;
-    const float x1 = bf(src[i]), x2 = bf(src[i + half]);
-    kt[(hb * hd + i) * L + p] = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
-    kt[(hb * hd + i + half) * L + p] = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
-    const uint16_t* vs = v + (size_t)bt * ldv + (size_t)kh * hd;
-    vc[(hb * L + p) * hd + i] = vs[i];
-    vc[(hb * L + p) * hd + i + half] = vs[i + half];
+    for (int e = threadIdx.x; e < cnt * half; e += blockDim.x) {
+        const int tl = e / half, i = e - tl * half, t = t0 + tl;
+        const size_t bt = (size_t)b * T + t;
+        const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+        const uint16_t* src = is_q ? q + bt * ldq + (size_t)head * hd : k + bt * ldk + (size_t)kh * hd;
+        const float x1 = bf(src[i]), x2 = bf(src[i + half]);
+        const uint16_t r1 = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
+        const uint16_t r2 = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
+        if (is_q) {
+            uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
+            dst[i] = r1;
+            dst[i + half] = r2;
+        } else {
+            tile[i * (RP_T + 2) + tl] = r1;
+            tile[(i + half) * (RP_T + 2) + tl] = r2;
+            const uint16_t* vs = v + bt * ldv + (size_t)kh * hd;
+            uint16_t* vd = vc + (hb * L + start + t) * hd;
+            vd[i] = vs[i];
+            vd[i + half] = vs[i + half];
+        }
+    }
+    if (is_q) return;                                         // uniform over the block
+    __syncthreads();
+    const int tl = threadIdx.x % RP_T;
+    for (int d = threadIdx.x / RP_T; d < hd; d += blockDim.x / RP_T)
+        if (tl < cnt) kt[(hb * hd + d) * L + start + t0 + tl] = tile[d * (RP_T + 2) + tl];
 }
 
 // Decode attention over cache positions 0..*pos, split over gridDim.y chunks of at most 64
@@ -427,6 +442,26 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // out = bf16(bf16(silu(g)) * u), silu(x) = x / (1 + exp(-x)) in fp32 (F.silu then the product of
 // MLP.forward), over rows of n elements: row r of g / u starts ld elements after row r - 1 (the
 // two halves of one fused projection), out is [rows, n].
+// Vector form: n % 8 == 0, ld % 8 == 0, 16-byte aligned rows; block (chunk of 256 x 8 elements, row).
+__global__ __launch_bounds__(256) void silu_mul8_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                        uint16_t* __restrict__ out, int n, int64_t ld) {
+    const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (c >= n) return;
+    const size_t r = blockIdx.y, i = r * ld + c;
+    const uint4 ga = *(const uint4*)(g + i), ua = *(const uint4*)(u + i);
+    const uint16_t* gs = (const uint16_t*)&ga;
+    const uint16_t* us = (const uint16_t*)&ua;
+    uint4 oa;
+    uint16_t* os = (uint16_t*)&oa;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float x = bf(gs[j]);
+        const float sv = bf(to_bf(__fdiv_rn(x, add_rn(1.f, expf(-x)))));
+        os[j] = to_bf(mul_rn(sv, bf(us[j])));
+    }
+    *(uint4*)(out + r * n + c) = oa;
+}
+
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                                 uint16_t* __restrict__ out, int rows, int n, int64_t ld) {
     const int64_t total = (int64_t)rows * n;
@@ -660,16 +695,17 @@ int tfp8_llm_attention(const float* qf, const void* kt, const void* vc, const in
 }
 
 // Rows of q / k / v: B * T, row r = b * T + t, ldq / ldk / ldv elements apart; 0 <= start and
-// start + T <= L.
+// start + T <= L; hd even and at most 256 (the key tile takes hd * (RP_T + 2) * 2 bytes of LDS).
 int tfp8_llm_rope_prefill(const void* q, const void* k, const void* v, const float* cs, const float* sn, void* qo,
                           void* kt, void* vc, int start, int B, int T, int H, int Hkv, int hd, int L, int ldq, int ldk,
                           int ldv, void* stream) {
-    if (B < 0 || T < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 512 || L <= 0) return -1;
+    if (B < 0 || T < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || hd > 256 || L <= 0) return -1;
     if (start < 0 || (int64_t)start + T > L || ldq < H * hd || ldk < Hkv * hd || ldv < Hkv * hd) return -1;
     if (!q || !k || !v || !cs || !sn || !qo || !kt || !vc) return -1;
     if (B == 0 || T == 0) return 0;
-    if ((int64_t)B * T > 65535) return -1;                    // gridDim.y
-    rope_prefill_kernel<<<dim3(H + Hkv, B * T), hd / 2, 0, (hipStream_t)stream>>>(
+    const int64_t tiles = (int64_t)B * ((T + RP_T - 1) / RP_T);
+    if (tiles > 65535) return -1;                             // gridDim.y
+    rope_prefill_kernel<<<dim3(H + Hkv, (unsigned)tiles), 256, (size_t)hd * (RP_T + 2) * 2, (hipStream_t)stream>>>(
         (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)qo, (uint16_t*)kt,
         (uint16_t*)vc, start, T, H, Hkv, hd, L, ldq, ldk, ldv);
     return launched();
@@ -703,6 +739,14 @@ int tfp8_llm_rope_attention(const void* q, const void* k, const void* v, const f
 int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int rows, int n, int64_t ld, void* stream) {
     if (rows < 0 || n < 0 || ld < n || !g || !u || !out) return -1;
     if (rows == 0 || n == 0) return 0;
+    // 8 elements a thread for many rows (prefill); a decoding step's few rows keep one element a thread,
+    // whose more threads finish sooner than a few blocks each evaluating 8 exp / divide in a row.
+    if (rows >= 64 && rows <= 65535 && n % 8 == 0 && ld % 8 == 0 &&
+        ((uintptr_t)g | (uintptr_t)u | (uintptr_t)out) % 16 == 0) {
+        silu_mul8_kernel<<<dim3((unsigned)((n / 8 + 255) / 256), (unsigned)rows), 256, 0, (hipStream_t)stream>>>(
+            (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, n, ld);
+        return launched();
+    }
     const int64_t blocks = ((int64_t)rows * n + 255) / 256;
     silu_mul_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)g, (const uint16_t*)u, (uint16_t*)out, rows, n, ld);

@@ -227,6 +227,9 @@ def test_llm_ops_match_pytorch_forms():
         gg = (3 * torch.randn(B, 1, 4 * d, device="cuda", generator=g)).bfloat16()
         uu = torch.randn(B, 1, 4 * d, device="cuda", generator=g).bfloat16()
         assert _bf16_ulps(ops.silu_mul(gg, uu), torch.nn.functional.silu(gg) * uu).max().item() <= 1
+        g1 = (3 * torch.randn(80, 2 * 1024, device="cuda", generator=g)).bfloat16()   # 80 rows: 8-wide form
+        assert _bf16_ulps(ops.silu_mul(g1[:, :1024], g1[:, 1024:]),
+                          torch.nn.functional.silu(g1[:, :1024]) * g1[:, 1024:]).max().item() <= 1
 
         # rotary + cache write at position p, and attention over 0..p, against the static step's
         # PyTorch ops (Attention.forward_static with the same caches)
@@ -319,7 +322,7 @@ def test_rope_prefill_matches_pytorch_form():
     from tfp8.examples import llm_ops as ops
     g = torch.Generator("cuda").manual_seed(13)
     for B, T, start, L, H, Hkv, hd in ((2, 37, 5, 64, 8, 4, 128), (1, 512, 0, 512, 16, 16, 128),
-                                       (3, 1, 90, 100, 4, 2, 64)):
+                                       (3, 1, 90, 100, 4, 2, 64), (2, 100, 3, 128, 4, 4, 256)):
         print(f"[rope_prefill] B={B} T={T} start={start} L={L} H={H} Hkv={Hkv} hd={hd}", flush=True)
         qkv = torch.randn(B, T, (H + 2 * Hkv) * hd, device="cuda", generator=g).bfloat16()
         q, k, v = qkv[..., :H * hd], qkv[..., H * hd:(H + Hkv) * hd], qkv[..., (H + Hkv) * hd:]
