@@ -85,7 +85,17 @@ class Attention(nn.Module):
 
     def attend(self, q, kt, vc, start):
         """Causal attention of the rotated queries q [B, H, T, hd] (positions start .. start + T - 1)
-        over cache positions 0 .. start + T - 1, then o_proj; returns [B, T, dim] in q's dtype."""
+        over cache positions 0 .. start + T - 1, then o_proj; returns [B, T, dim] in q's dtype.  On
+        the GPU (bf16, hd = 128, a cache length that is a multiple of 8) one flash-attention kernel
+        (llm_ops.attn_prefill) computes what attend_torch does with about 15 PyTorch kernels."""
+        if q.is_cuda and q.dtype == kt.dtype == torch.bfloat16 and self.hd == 128 and kt.shape[3] % 8 == 0:
+            from tfp8.examples import llm_ops as ops
+            return self.o_proj(ops.attn_prefill(q.contiguous(), kt, vc, start, self.nh, self.nkv))
+        return self.attend_torch(q, kt, vc, start)
+
+    def attend_torch(self, q, kt, vc, start):
+        """attend as PyTorch ops: fp32 scores (bf16 q . k products with fp32 sums on the GPU), the
+        causal mask, fp32 softmax and fp32 value product."""
         B, _, T, _ = q.shape
         L = start + T
         rep = self.nh // self.nkv

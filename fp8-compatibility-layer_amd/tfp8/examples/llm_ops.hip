@@ -539,6 +539,129 @@ __global__ __launch_bounds__(256) void head_mfma_kernel(const uint16_t* __restri
     }
 }
 
+// Causal attention of the prefill (Attention.attend: softmax((q . k) / sqrt(hd), key <= query) times
+// v, for the T query positions start .. start + T - 1 over cache positions 0 .. start + T - 1) as one
+// flash-attention kernel, hd = 128.  Block (query tile of 64 rows, head, batch), 4 waves of 16 rows;
+// per step of 64 cache positions the key tile is staged in LDS as [position][dim] and the value tile
+// as [dim][position] (the caches hold them the other way round for the decoding kernels), then per
+// wave, with v_mfma_f32_16x16x32_bf16:
+//   S^T = K Q^T   (A: 16 positions x 8 dims per lane from LDS; B: the wave's q rows, in registers),
+//   O^T += V^T P^T (A: 16 dims x 8 positions per lane from LDS; B: P^T straight from S^T's lanes).
+// Lane l ends S^T holding positions 16 mt + 4 (l >> 4) + r of query row l & 15, so P^T needs no
+// shuffle: the O^T product takes its 32 positions per step in that order (the same order on both
+// operands, so the sum is unchanged), and O^T lands with query row l & 15 in the lane that holds
+// that row's softmax statistics.  bf16 x bf16 products are exact and summed in fp32, as the bf16
+// score product with fp32 output; P (fp32) enters the value product as bf16 hi + lo (2^-18 relative),
+// the values being bf16; the running max / sum rescale as in any online softmax.  Positions past
+// the written ones read as zeros (the cache may hold anything there) and are masked with -inf.
+constexpr int FA_KP = 136;   // key tile row pitch in elements: 128 dims + 8
+constexpr int FA_VP = 72;    // value tile row pitch: 64 positions + 8
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kt,
+                                                           const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+                                                           int start, int T, int H, int Hkv, int Lc, int ldo, float scale) {
+    __shared__ __align__(16) uint16_t ks[64 * FA_KP];
+    __shared__ __align__(16) uint16_t vt[128 * FA_VP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15, g = lane >> 4;
+    const int nT = (T + 63) / 64, tile = nT - 1 - (int)blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t0 = tile * 64, row = t0 + 16 * wave + j, qp = start + row;
+    const int kmax = start + min(t0 + 63, T - 1);             // last position the tile's rows see
+    const size_t hb = (size_t)b * Hkv + h / (H / Hkv);
+    hbf16x8 qb[4];
+    const uint16_t* qrow = q + (((size_t)b * H + h) * T + min(row, T - 1)) * 128;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qb[k] = __builtin_bit_cast(hbf16x8, *(const uint4*)(qrow + 32 * k + 8 * g));
+    float m_run = -INFINITY, l_run = 0.f;
+    hf32x4 o[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] = hf32x4{0.f, 0.f, 0.f, 0.f};
+    const int nk = kmax / 64 + 1;
+    for (int kb = 0; kb < nk; ++kb) {
+        const int p0 = kb * 64;
+        __syncthreads();                                      // the previous step's tiles are read
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {                      // keys: kt[dim][p .. p + 7] -> ks[p + i][dim]
+            const int e = tid + 256 * it, d = e >> 3, p = p0 + 8 * (e & 7);
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (p <= kmax) v = *(const uint4*)(kt + (hb * 128 + d) * Lc + p);
+            const uint16_t* vs = (const uint16_t*)&v;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ks[(p - p0 + i) * FA_KP + d] = vs[i];
+        }
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {                      // values: vc[p][d .. d + 7] -> vt[d + i][p]
+            const int e = tid + 256 * it, pl = e >> 4, d = 8 * (e & 15);
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (p0 + pl <= kmax) v = *(const uint4*)(vc + (hb * Lc + p0 + pl) * 128 + d);
+            const uint16_t* vs = (const uint16_t*)&v;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vt[(d + i) * FA_VP + pl] = vs[i];
+        }
+        __syncthreads();
+        hf32x4 sc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            sc[mt] = hf32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    *(const hbf16x8*)(ks + (16 * mt + j) * FA_KP + 32 * k + 8 * g), qb[k], sc[mt], 0, 0, 0);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = mul_rn(sc[mt][r], scale);
+                sc[mt][r] = p0 + 16 * mt + 4 * g + r > qp ? -INFINITY : v;
+                mx = fmaxf(mx, sc[mt][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);                 // finite: position 0 is in every row's first step
+        const float alpha = expf(sub_rn(m_run, m_new));
+        float ps = 0.f;
+        alignas(16) uint16_t hi[2][8], lo[2][8];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pv = expf(sub_rn(sc[mt][r], m_new));
+                ps = add_rn(ps, pv);
+                const uint16_t ph = to_bf(pv);
+                hi[mt >> 1][(mt & 1) * 4 + r] = ph;
+                lo[mt >> 1][(mt & 1) * 4 + r] = to_bf(sub_rn(pv, bf(ph)));
+            }
+        ps = add_rn(ps, __shfl_xor(ps, 16));
+        ps = add_rn(ps, __shfl_xor(ps, 32));
+        l_run = add_rn(mul_rn(l_run, alpha), ps);
+        m_run = m_new;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) o[mt] *= alpha;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const hbf16x8 bh = __builtin_bit_cast(hbf16x8, *(const uint4*)hi[k]);
+            const hbf16x8 bl = __builtin_bit_cast(hbf16x8, *(const uint4*)lo[k]);
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt) {
+                const uint16_t* vr = vt + (16 * mt + j) * FA_VP + 32 * k + 4 * g;
+                const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
+                const hbf16x8 a = __builtin_bit_cast(hbf16x8, uint4{a0.x, a0.y, a1.x, a1.y});
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, o[mt], 0, 0, 0);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, o[mt], 0, 0, 0);
+            }
+        }
+    }
+    if (row >= T) return;
+    uint16_t* orow = out + ((size_t)b * T + row) * ldo + (size_t)h * 128;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+        alignas(8) uint16_t w[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] = to_bf(__fdiv_rn(o[mt][r], l_run));
+        *(uint2*)(orow + 16 * mt + 4 * g) = *(const uint2*)w;
+    }
+}
+
 // Start of a decode step (Llama.decode_step's embedding lookup and rotary angles): block b < B copies
 // embedding row tok[b] (bf16 [V, d]) into x[b] (a token outside 0..V-1 gives a zero row); block B
 // computes the angles pos * inv[i] in fp32 and their cosine and sine, as pos.float() * inv, .cos()
@@ -753,6 +876,20 @@ int tfp8_llm_silu_mul(const void* g, const void* u, void* out, int rows, int n, 
     return launched();
 }
 
+
+// q bf16 [B, H, T, 128] contiguous, caches kt [B, Hkv, 128, Lc] / vc [B, Hkv, Lc, 128] (Lc % 8 == 0),
+// out bf16 rows b * T + t of ldo elements (ldo % 4 == 0, >= H * 128); 16-byte aligned pointers.
+int tfp8_llm_attn_prefill(const void* q, const void* kt, const void* vc, void* out, int start, int B, int T, int H,
+                          int Hkv, int hd, int Lc, int ldo, float scale, void* stream) {
+    if (B < 0 || T < 0 || H <= 0 || Hkv <= 0 || H % Hkv || hd != 128 || Lc <= 0 || Lc % 8) return -1;
+    if (start < 0 || (int64_t)start + T > Lc || ldo < H * 128 || ldo % 4 || !q || !kt || !vc || !out) return -1;
+    if (((uintptr_t)q | (uintptr_t)kt | (uintptr_t)vc | (uintptr_t)out) % 16) return -1;
+    if (B == 0 || T == 0) return 0;
+    if (B > 65535 || H > 65535) return -1;
+    attn_prefill_kernel<<<dim3((unsigned)((T + 63) / 64), (unsigned)H, (unsigned)B), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)q, (const uint16_t*)kt, (const uint16_t*)vc, (uint16_t*)out, start, T, H, Hkv, Lc, ldo, scale);
+    return launched();
+}
 
 // rows <= 16, K % 512 == 0, V * K * 2 < 2^31.
 int tfp8_llm_head(const void* x, const void* w, float* y, int rows, int V, int K, void* stream) {

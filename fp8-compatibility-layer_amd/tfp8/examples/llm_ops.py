@@ -2,12 +2,13 @@
 
 Each function takes CUDA tensors, checks their shapes and dtypes, launches on torch's current
 stream (so the calls record into a HIP graph under capture) and returns new output tensors.  The
-library is the example model's own code; demo_llm uses it for the decode step on the GPU and raises
-if it is missing there."""
+library is the example model's own code; demo_llm uses it for the decode step and the prefill on
+the GPU and raises if it is missing there."""
 import ctypes
 import math
 import os
 
+import numpy as np
 import torch
 
 _PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtfp8_llm.so")
@@ -30,6 +31,7 @@ def library():
         lib.tfp8_llm_step_in.argtypes = [p, p, p, p, p, p, p, i, i, i, i, p]
         lib.tfp8_llm_step_out.argtypes = [p, i, i, i64, p, p, p]
         lib.tfp8_llm_rope_prefill.argtypes = [p, p, p, p, p, p, p, p, i, i, i, i, i, i, i, i, i, i, p]
+        lib.tfp8_llm_attn_prefill.argtypes = [p, p, p, p, i, i, i, i, i, i, i, i, f, p]
         for fn in (lib.tfp8_llm_add_rmsnorm, lib.tfp8_llm_rope_cache, lib.tfp8_llm_attention, lib.tfp8_llm_silu_mul,
                    lib.tfp8_llm_head, lib.tfp8_llm_rope_attention, lib.tfp8_llm_step_in, lib.tfp8_llm_step_out):
             fn.restype = ctypes.c_int
@@ -181,6 +183,27 @@ def rope_prefill(q, k, v, cos, sin, kt, vc, start, n_heads, n_kv):
                                            qo.data_ptr(), kt.data_ptr(), vc.data_ptr(), int(start), B, T, n_heads,
                                            n_kv, hd, L, ldq, ldk, ldv, _stream(q)), "rope_prefill")
     return qo
+
+
+def attn_prefill(q, kt, vc, start, n_heads, n_kv):
+    """Causal attention of the rotated queries q (bf16 [B, n_heads, T, 128], positions start ..
+    start + T - 1) over the bf16 caches kt [B, n_kv, 128, L] / vc [B, n_kv, L, 128] (L % 8 == 0),
+    positions 0 .. start + T - 1: softmax((q . k) / sqrt(128), key <= query) times v, fp32 inside;
+    returns bf16 [B, T, n_heads * 128] (the rows o_proj takes)."""
+    _bf16(q, "q")
+    _bf16(kt, "kt")
+    _bf16(vc, "vc")
+    B, H, T, hd = q.shape
+    L = kt.shape[3]
+    if H != n_heads or hd != 128 or tuple(kt.shape) != (B, n_kv, hd, L) or tuple(vc.shape) != (B, n_kv, L, hd):
+        raise ValueError(f"q {tuple(q.shape)}, caches {tuple(kt.shape)} / {tuple(vc.shape)}")
+    if L % 8 or not 0 <= start <= L - T:
+        raise ValueError(f"cache of {L} positions (a multiple of 8), positions {start} .. {start + T - 1}")
+    out = torch.empty(B, T, H * hd, dtype=torch.bfloat16, device=q.device)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(hd)))     # fp32 reciprocal of the divisor
+    _check(library().tfp8_llm_attn_prefill(q.data_ptr(), kt.data_ptr(), vc.data_ptr(), out.data_ptr(), int(start), B,
+                                           T, H, n_kv, hd, L, H * hd, scale, _stream(q)), "attn_prefill")
+    return out
 
 
 def silu_mul(g, u):

@@ -342,6 +342,39 @@ def test_rope_prefill_matches_pytorch_form():
         assert torch.equal(kt, kt2) and torch.equal(vc, vc2)
 
 
+def test_attn_prefill_matches_fp32_attention():
+    """attn_prefill (the prefill's causal attention as one flash-attention kernel) against the same
+    attention in fp32 PyTorch ops (fp32 scores of the widened bf16 values, -inf above the diagonal,
+    softmax, fp32 value product) within bf16 rounding of the fp32 result: grouped and ungrouped
+    heads, query tiles that end inside a 64-row tile, a prefill that starts after cached positions,
+    a single position, and cache positions past the written ones holding NaN (never read into the
+    result)."""
+    import math
+    from tfp8.examples import llm_ops as ops
+    g = torch.Generator("cuda").manual_seed(17)
+    hd = 128
+    for B, H, Hkv, T, start, Lc in ((2, 8, 4, 100, 0, 104), (1, 4, 4, 64, 37, 112), (3, 4, 2, 1, 90, 96),
+                                    (1, 16, 16, 512, 0, 512), (2, 4, 1, 130, 7, 144)):
+        print(f"[attn_prefill] B={B} H={H} Hkv={Hkv} T={T} start={start} Lc={Lc}", flush=True)
+        Lw = start + T
+        q = torch.randn(B, H, T, hd, device="cuda", generator=g).bfloat16()
+        kt = torch.randn(B, Hkv, hd, Lc, device="cuda", generator=g).bfloat16()
+        vc = torch.randn(B, Hkv, Lc, hd, device="cuda", generator=g).bfloat16()
+        kt[..., Lw:] = float("nan")
+        vc[:, :, Lw:] = float("nan")
+        with torch.no_grad():
+            o = ops.attn_prefill(q, kt, vc, start, H, Hkv)
+            rep = H // Hkv
+            sc = torch.matmul(q.float(), kt[..., :Lw].float().repeat_interleave(rep, 1)) / math.sqrt(hd)
+            qpos = torch.arange(start, Lw, device="cuda")[:, None]
+            sc = sc.masked_fill(torch.arange(Lw, device="cuda")[None, :] > qpos, float("-inf"))
+            ref = torch.matmul(torch.softmax(sc, -1), vc[:, :, :Lw].float().repeat_interleave(rep, 1))
+            ref = ref.transpose(1, 2).reshape(B, T, H * hd)
+        assert o.shape == (B, T, H * hd) and bool(torch.isfinite(o).all())
+        err = (o.float() - ref).abs()
+        assert (err <= 2.0 ** -8 * ref.abs() + 1e-5).all(), err.max().item()
+
+
 def test_step_in_and_step_out_match_pytorch_forms():
     """The decode step's own start and end as one kernel each, against decode_step's PyTorch ops bit
     for bit: the embedding rows of the tokens and cos / sin of pos.float() * inv (step_in); the

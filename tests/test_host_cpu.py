@@ -332,12 +332,13 @@ def test_abi_argument_validation_without_gpu():
 
 
 def test_example_ops_library_loads_and_validates_without_gpu():
-    """libtfp8_llm.so (the example model's fused ops) exports its nine entry points and
+    """libtfp8_llm.so (the example model's fused ops) exports its ten entry points and
     refuses arguments its kernels do not take before launching anything."""
     from tfp8.examples import llm_ops
     lib = llm_ops.library()
     for n in ("tfp8_llm_add_rmsnorm", "tfp8_llm_rope_cache", "tfp8_llm_attention", "tfp8_llm_silu_mul", "tfp8_llm_head",
-              "tfp8_llm_rope_attention", "tfp8_llm_step_in", "tfp8_llm_step_out", "tfp8_llm_rope_prefill"):
+              "tfp8_llm_rope_attention", "tfp8_llm_step_in", "tfp8_llm_step_out", "tfp8_llm_rope_prefill",
+              "tfp8_llm_attn_prefill"):
         assert hasattr(lib, n), n
     buf = ctypes.create_string_buffer(4096)
     a = (ctypes.addressof(buf) + 255) & ~255
@@ -361,6 +362,10 @@ def test_example_ops_library_loads_and_validates_without_gpu():
     assert lib.tfp8_llm_rope_prefill(a, a, a, a, a, a, a, a, 0, 1, 8, 8, 4, 128, 64, 512, 512, 512,
                                      None) == -1                       # ldq < H hd
     assert lib.tfp8_llm_rope_prefill(a, a, a, a, a, a, a, a, 0, 1, 0, 8, 4, 128, 64, 1024, 512, 512, None) == 0
+    assert lib.tfp8_llm_attn_prefill(a, a, a, a, 0, 1, 8, 4, 4, 64, 64, 512, 1.0, None) == -1    # head dim 64
+    assert lib.tfp8_llm_attn_prefill(a, a, a, a, 0, 1, 8, 4, 4, 128, 60, 512, 1.0, None) == -1   # L % 8
+    assert lib.tfp8_llm_attn_prefill(a, a, a, a, 60, 1, 8, 4, 4, 128, 64, 512, 1.0, None) == -1  # start + T > L
+    assert lib.tfp8_llm_attn_prefill(a, a, a, a, 0, 1, 0, 4, 4, 128, 64, 512, 1.0, None) == 0
 
 
 def test_demo_fused_projections_share_the_layers_weights():
