@@ -574,6 +574,27 @@ def graph_decode(size="c5", B=1, prompt_len=512, n_decode=128):
     return ms
 
 
+def prefill_only(size="c5", B=1, prompt_len=512, reps=5):
+    """Only the FP8 model's eager prefill (for kernel profiles): convert, 4 warm-up forwards (past
+    the NaN-watched first calls of every layer), then `reps` timed forwards; returns ms each."""
+    from tfp8 import FP8Config, prepare_model
+    model = build(size)
+    prepare_model(model, "llm", FP8Config(profile="llm_safe", fmt="e4m3fn"))
+    ids = torch.randint(0, model.c["vocab"], (B, prompt_len), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+    cache = model.new_cache(B, prompt_len + 8)
+    with torch.no_grad():
+        for _ in range(4):
+            model(ids, cache, 0)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            model(ids, cache, 0)
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / reps
+    print(f"{size} B={B}: eager prefill {ms:.3f} ms over {reps} forwards of {prompt_len} tokens")
+    return ms
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--size", default="c5", choices=list(SIZES))
@@ -581,8 +602,12 @@ if __name__ == "__main__":
     ap.add_argument("--decode", type=int, default=128)
     ap.add_argument("--graph-decode", type=int, default=None, metavar="B",
                     help="only time the FP8 model's graph decode at batch B (for kernel profiles)")
+    ap.add_argument("--prefill", type=int, default=None, metavar="B",
+                    help="only time the FP8 model's eager prefill at batch B (for kernel profiles)")
     a = ap.parse_args()
-    if a.graph_decode:
+    if a.prefill:
+        prefill_only(a.size, a.prefill, a.prompt_len)
+    elif a.graph_decode:
         graph_decode(a.size, a.graph_decode, a.prompt_len, a.decode)
     else:
         run(a.size, a.prompt_len, a.decode)

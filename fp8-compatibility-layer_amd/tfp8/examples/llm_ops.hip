@@ -162,25 +162,45 @@ __global__ __launch_bounds__(256) void rope_prefill_kernel(const uint16_t* __res
     const bool is_q = head < H;
     const int kh = head - H;
     const size_t hb = (size_t)b * Hkv + kh;
-    for (int e = threadIdx.x; e < cnt * half; e += blockDim.x) {
-        const int tl = e / half, i = e - tl * half, t = t0 + tl;
-        const size_t bt = (size_t)b * T + t;
-        const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
-        const uint16_t* src = is_q ? q + bt * ldq + (size_t)head * hd : k + bt * ldk + (size_t)kh * hd;
-        const float x1 = bf(src[i]), x2 = bf(src[i + half]);
-        const uint16_t r1 = to_bf(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
-        const uint16_t r2 = to_bf(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
-        if (is_q) {
-            uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
-            dst[i] = r1;
-            dst[i + half] = r2;
-        } else {
-            tile[i * (RP_T + 2) + tl] = r1;
-            tile[(i + half) * (RP_T + 2) + tl] = r2;
-            const uint16_t* vs = v + bt * ldv + (size_t)kh * hd;
-            uint16_t* vd = vc + (hb * L + start + t) * hd;
-            vd[i] = vs[i];
-            vd[i + half] = vs[i + half];
+    const int n = cnt * half;
+    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * blockDim.x) {   // four elements' loads in flight
+        float c[4], sv[4], x1[4], x2[4];
+        uint16_t v1[4], v2[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            if (e >= n) break;
+            const int tl = e / half, i = e - tl * half, t = t0 + tl;
+            const size_t bt = (size_t)b * T + t;
+            c[u] = cs[(size_t)t * half + i];
+            sv[u] = sn[(size_t)t * half + i];
+            const uint16_t* src = is_q ? q + bt * ldq + (size_t)head * hd : k + bt * ldk + (size_t)kh * hd;
+            x1[u] = bf(src[i]);
+            x2[u] = bf(src[i + half]);
+            if (!is_q) {
+                const uint16_t* vs = v + bt * ldv + (size_t)kh * hd;
+                v1[u] = vs[i];
+                v2[u] = vs[i + half];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            if (e >= n) break;
+            const int tl = e / half, i = e - tl * half, t = t0 + tl;
+            const uint16_t r1 = to_bf(sub_rn(mul_rn(x1[u], c[u]), mul_rn(x2[u], sv[u])));
+            const uint16_t r2 = to_bf(add_rn(mul_rn(x2[u], c[u]), mul_rn(x1[u], sv[u])));
+            if (is_q) {
+                uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
+                dst[i] = r1;
+                dst[i + half] = r2;
+            } else {
+                tile[i * (RP_T + 2) + tl] = r1;
+                tile[(i + half) * (RP_T + 2) + tl] = r2;
+                uint16_t* vd = vc + (hb * L + start + t) * hd;
+                vd[i] = v1[u];
+                vd[i + half] = v2[u];
+            }
         }
     }
     if (is_q) return;                                         // uniform over the block
@@ -578,23 +598,33 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
     for (int kb = 0; kb < nk; ++kb) {
         const int p0 = kb * 64;
         __syncthreads();                                      // the previous step's tiles are read
+        {   // keys: thread (dims 4 dg .. + 3, positions 8 pg .. + 7): 4 rows of kt in, 8 positions x 4 dims out
+            const int dg = tid & 31, pg = tid >> 5, p = p0 + 8 * pg;
+            uint4 r4[4];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {                      // keys: kt[dim][p .. p + 7] -> ks[p + i][dim]
-            const int e = tid + 256 * it, d = e >> 3, p = p0 + 8 * (e & 7);
-            uint4 v = {0u, 0u, 0u, 0u};
-            if (p <= kmax) v = *(const uint4*)(kt + (hb * 128 + d) * Lc + p);
-            const uint16_t* vs = (const uint16_t*)&v;
+            for (int r = 0; r < 4; ++r)
+                r4[r] = p <= kmax ? *(const uint4*)(kt + (hb * 128 + 4 * dg + r) * Lc + p) : uint4{0u, 0u, 0u, 0u};
+            const uint16_t* rs = (const uint16_t*)r4;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ks[(p - p0 + i) * FA_KP + d] = vs[i];
+            for (int i = 0; i < 8; ++i) {
+                alignas(8) uint16_t w[4] = {rs[i], rs[8 + i], rs[16 + i], rs[24 + i]};
+                *(uint2*)(ks + (8 * pg + i) * FA_KP + 4 * dg) = *(const uint2*)w;
+            }
         }
+        {   // values: thread (positions 4 pg .. + 3, dims 8 dg .. + 7): 4 rows of vc in, 8 dims x 4 positions out
+            const int dg = tid & 15, pg = tid >> 4;
+            uint4 r4[4];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {                      // values: vc[p][d .. d + 7] -> vt[d + i][p]
-            const int e = tid + 256 * it, pl = e >> 4, d = 8 * (e & 15);
-            uint4 v = {0u, 0u, 0u, 0u};
-            if (p0 + pl <= kmax) v = *(const uint4*)(vc + (hb * Lc + p0 + pl) * 128 + d);
-            const uint16_t* vs = (const uint16_t*)&v;
+            for (int r = 0; r < 4; ++r) {
+                const int pp = p0 + 4 * pg + r;
+                r4[r] = pp <= kmax ? *(const uint4*)(vc + (hb * Lc + pp) * 128 + 8 * dg) : uint4{0u, 0u, 0u, 0u};
+            }
+            const uint16_t* rs = (const uint16_t*)r4;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vt[(d + i) * FA_VP + pl] = vs[i];
+            for (int i = 0; i < 8; ++i) {
+                alignas(8) uint16_t w[4] = {rs[i], rs[8 + i], rs[16 + i], rs[24 + i]};
+                *(uint2*)(vt + (8 * dg + i) * FA_VP + 4 * pg) = *(const uint2*)w;
+            }
         }
         __syncthreads();
         hf32x4 sc[4];
