@@ -595,38 +595,39 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) o[mt] = hf32x4{0.f, 0.f, 0.f, 0.f};
     const int nk = kmax / 64 + 1;
+    // Tile rows for the LDS staging: keys as (dims 4 kdg .. + 3, positions 8 kpg .. + 7), values as
+    // (positions 4 vpg .. + 3, dims 8 vdg .. + 7); the next step's rows load while this one computes.
+    const int kdg = tid & 31, kpg = tid >> 5, vdg = tid & 15, vpg = tid >> 4;
+    uint4 kr[4], vr[4];
+    auto load = [&](int p0) {
+        const int p = p0 + 8 * kpg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            kr[r] = p <= kmax ? *(const uint4*)(kt + (hb * 128 + 4 * kdg + r) * Lc + p) : uint4{0u, 0u, 0u, 0u};
+            const int pp = p0 + 4 * vpg + r;
+            vr[r] = pp <= kmax ? *(const uint4*)(vc + (hb * Lc + pp) * 128 + 8 * vdg) : uint4{0u, 0u, 0u, 0u};
+        }
+    };
+    load(0);
     for (int kb = 0; kb < nk; ++kb) {
         const int p0 = kb * 64;
         __syncthreads();                                      // the previous step's tiles are read
-        {   // keys: thread (dims 4 dg .. + 3, positions 8 pg .. + 7): 4 rows of kt in, 8 positions x 4 dims out
-            const int dg = tid & 31, pg = tid >> 5, p = p0 + 8 * pg;
-            uint4 r4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                r4[r] = p <= kmax ? *(const uint4*)(kt + (hb * 128 + 4 * dg + r) * Lc + p) : uint4{0u, 0u, 0u, 0u};
-            const uint16_t* rs = (const uint16_t*)r4;
+        {
+            const uint16_t* rs = (const uint16_t*)kr;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 alignas(8) uint16_t w[4] = {rs[i], rs[8 + i], rs[16 + i], rs[24 + i]};
-                *(uint2*)(ks + (8 * pg + i) * FA_KP + 4 * dg) = *(const uint2*)w;
+                *(uint2*)(ks + (8 * kpg + i) * FA_KP + 4 * kdg) = *(const uint2*)w;
             }
-        }
-        {   // values: thread (positions 4 pg .. + 3, dims 8 dg .. + 7): 4 rows of vc in, 8 dims x 4 positions out
-            const int dg = tid & 15, pg = tid >> 4;
-            uint4 r4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int pp = p0 + 4 * pg + r;
-                r4[r] = pp <= kmax ? *(const uint4*)(vc + (hb * Lc + pp) * 128 + 8 * dg) : uint4{0u, 0u, 0u, 0u};
-            }
-            const uint16_t* rs = (const uint16_t*)r4;
+            const uint16_t* vs = (const uint16_t*)vr;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                alignas(8) uint16_t w[4] = {rs[i], rs[8 + i], rs[16 + i], rs[24 + i]};
-                *(uint2*)(vt + (8 * dg + i) * FA_VP + 4 * pg) = *(const uint2*)w;
+                alignas(8) uint16_t w[4] = {vs[i], vs[8 + i], vs[16 + i], vs[24 + i]};
+                *(uint2*)(vt + (8 * vdg + i) * FA_VP + 4 * vpg) = *(const uint2*)w;
             }
         }
         __syncthreads();
+        if (kb + 1 < nk) load(p0 + 64);
         hf32x4 sc[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
