@@ -151,6 +151,7 @@ __global__ void rope_cache_kernel(const uint16_t* __restrict__ q, const uint16_t
 // thread would scatter 2-byte stores L elements apart); the value head goes straight to vc [B, Hkv,
 // L, hd] rows.  The same operations as rope_cache_kernel, so the same bits as the PyTorch form.
 constexpr int RP_T = 64;
+template <int V>   // V consecutive dims per thread (V = 4: 8-byte q / k / v and 16-byte cos / sin accesses)
 __global__ __launch_bounds__(256) void rope_prefill_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                            const uint16_t* __restrict__ v, const float* __restrict__ cs,
                                                            const float* __restrict__ sn, uint16_t* __restrict__ qo,
@@ -158,48 +159,58 @@ __global__ __launch_bounds__(256) void rope_prefill_kernel(const uint16_t* __res
                                                            int T, int H, int Hkv, int hd, int L, int ldq, int ldk, int ldv) {
     extern __shared__ uint16_t tile[];                        // [hd][RP_T + 2]
     const int nt = (T + RP_T - 1) / RP_T, head = blockIdx.x, b = blockIdx.y / nt;
-    const int t0 = (blockIdx.y - b * nt) * RP_T, cnt = min(RP_T, T - t0), half = hd / 2;
+    const int t0 = (blockIdx.y - b * nt) * RP_T, cnt = min(RP_T, T - t0), half = hd / 2, hv = half / V;
     const bool is_q = head < H;
     const int kh = head - H;
     const size_t hb = (size_t)b * Hkv + kh;
-    const int n = cnt * half;
-    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * blockDim.x) {   // four elements' loads in flight
-        float c[4], sv[4], x1[4], x2[4];
-        uint16_t v1[4], v2[4];
+    const int n = cnt * hv;
+    typedef uint16_t u16v __attribute__((ext_vector_type(V)));
+    typedef float f32v __attribute__((ext_vector_type(V)));
+    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * blockDim.x) {   // four loads of each kind in flight
+        f32v c[4], sv[4];
+        u16v x1[4], x2[4], v1[4], v2[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = e0 + u * (int)blockDim.x;
             if (e >= n) break;
-            const int tl = e / half, i = e - tl * half, t = t0 + tl;
+            const int tl = e / hv, i = (e - tl * hv) * V, t = t0 + tl;
             const size_t bt = (size_t)b * T + t;
-            c[u] = cs[(size_t)t * half + i];
-            sv[u] = sn[(size_t)t * half + i];
+            c[u] = *(const f32v*)(cs + (size_t)t * half + i);
+            sv[u] = *(const f32v*)(sn + (size_t)t * half + i);
             const uint16_t* src = is_q ? q + bt * ldq + (size_t)head * hd : k + bt * ldk + (size_t)kh * hd;
-            x1[u] = bf(src[i]);
-            x2[u] = bf(src[i + half]);
+            x1[u] = *(const u16v*)(src + i);
+            x2[u] = *(const u16v*)(src + i + half);
             if (!is_q) {
                 const uint16_t* vs = v + bt * ldv + (size_t)kh * hd;
-                v1[u] = vs[i];
-                v2[u] = vs[i + half];
+                v1[u] = *(const u16v*)(vs + i);
+                v2[u] = *(const u16v*)(vs + i + half);
             }
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = e0 + u * (int)blockDim.x;
             if (e >= n) break;
-            const int tl = e / half, i = e - tl * half, t = t0 + tl;
-            const uint16_t r1 = to_bf(sub_rn(mul_rn(x1[u], c[u]), mul_rn(x2[u], sv[u])));
-            const uint16_t r2 = to_bf(add_rn(mul_rn(x2[u], c[u]), mul_rn(x1[u], sv[u])));
+            const int tl = e / hv, i = (e - tl * hv) * V, t = t0 + tl;
+            u16v r1, r2;
+#pragma unroll
+            for (int w = 0; w < V; ++w) {
+                const float a = bf(x1[u][w]), bb = bf(x2[u][w]);
+                r1[w] = to_bf(sub_rn(mul_rn(a, c[u][w]), mul_rn(bb, sv[u][w])));
+                r2[w] = to_bf(add_rn(mul_rn(bb, c[u][w]), mul_rn(a, sv[u][w])));
+            }
             if (is_q) {
                 uint16_t* dst = qo + (((size_t)b * H + head) * T + t) * hd;
-                dst[i] = r1;
-                dst[i + half] = r2;
+                *(u16v*)(dst + i) = r1;
+                *(u16v*)(dst + i + half) = r2;
             } else {
-                tile[i * (RP_T + 2) + tl] = r1;
-                tile[(i + half) * (RP_T + 2) + tl] = r2;
+#pragma unroll
+                for (int w = 0; w < V; ++w) {
+                    tile[(i + w) * (RP_T + 2) + tl] = r1[w];
+                    tile[(i + w + half) * (RP_T + 2) + tl] = r2[w];
+                }
                 uint16_t* vd = vc + (hb * L + start + t) * hd;
-                vd[i] = v1[u];
-                vd[i + half] = v2[u];
+                *(u16v*)(vd + i) = v1[u];
+                *(u16v*)(vd + i + half) = v2[u];
             }
         }
     }
@@ -859,9 +870,20 @@ int tfp8_llm_rope_prefill(const void* q, const void* k, const void* v, const flo
     if (B == 0 || T == 0) return 0;
     const int64_t tiles = (int64_t)B * ((T + RP_T - 1) / RP_T);
     if (tiles > 65535) return -1;                             // gridDim.y
-    rope_prefill_kernel<<<dim3(H + Hkv, (unsigned)tiles), 256, (size_t)hd * (RP_T + 2) * 2, (hipStream_t)stream>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)qo, (uint16_t*)kt,
-        (uint16_t*)vc, start, T, H, Hkv, hd, L, ldq, ldk, ldv);
+    const dim3 grid(H + Hkv, (unsigned)tiles);
+    const size_t lds = (size_t)hd * (RP_T + 2) * 2;
+    // 4 dims a thread where every row and the cos / sin rows allow 8- / 16-byte accesses
+    const bool v4 = hd % 8 == 0 && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && L % 4 == 0 &&
+                    ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)qo | (uintptr_t)vc) % 8 == 0 &&
+                    ((uintptr_t)cs | (uintptr_t)sn) % 16 == 0;
+    if (v4)
+        rope_prefill_kernel<4><<<grid, 256, lds, (hipStream_t)stream>>>(
+            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)qo, (uint16_t*)kt,
+            (uint16_t*)vc, start, T, H, Hkv, hd, L, ldq, ldk, ldv);
+    else
+        rope_prefill_kernel<1><<<grid, 256, lds, (hipStream_t)stream>>>(
+            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cs, sn, (uint16_t*)qo, (uint16_t*)kt,
+            (uint16_t*)vc, start, T, H, Hkv, hd, L, ldq, ldk, ldv);
     return launched();
 }
 

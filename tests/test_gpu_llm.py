@@ -322,7 +322,8 @@ def test_rope_prefill_matches_pytorch_form():
     from tfp8.examples import llm_ops as ops
     g = torch.Generator("cuda").manual_seed(13)
     for B, T, start, L, H, Hkv, hd in ((2, 37, 5, 64, 8, 4, 128), (1, 512, 0, 512, 16, 16, 128),
-                                       (3, 1, 90, 100, 4, 2, 64), (2, 100, 3, 128, 4, 4, 256)):
+                                       (3, 1, 90, 100, 4, 2, 64), (2, 100, 3, 128, 4, 4, 256),
+                                       (1, 20, 2, 30, 2, 1, 128)):     # L % 4 != 0: one dim a thread
         print(f"[rope_prefill] B={B} T={T} start={start} L={L} H={H} Hkv={Hkv} hd={hd}", flush=True)
         qkv = torch.randn(B, T, (H + 2 * Hkv) * hd, device="cuda", generator=g).bfloat16()
         q, k, v = qkv[..., :H * hd], qkv[..., H * hd:(H + Hkv) * hd], qkv[..., (H + Hkv) * hd:]
